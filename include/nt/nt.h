@@ -1,0 +1,296 @@
+/*
+ * nt.h — C ABI of the MI355X (gfx950) neural-texture train/decode hot path.
+ *
+ * This header is the drop-in boundary. It replaces the reference's four C++ launchers
+ * (mavenkim2/neural_textures train.h:158-161):
+ *
+ *   void InvokeOptimizeNetwork(KernelParams);                    -> nt_optimize_network
+ *   void InvokeOptimizeFeatures(KernelParams, TrainingKernelType); -> nt_optimize_latents
+ *   void InvokeTraining(KernelParams, TrainingKernelType);       -> nt_train_step
+ *   void InvokeInference(KernelParams);                          -> nt_inference
+ *
+ * and adds the codec and decode entry points that the reference does not have
+ * (nt_codec_encode / nt_codec_decode / nt_decode), plus the tiny-MLP forward used by the
+ * reference's only unit test (tests/forward_pass_test.cu:15-32) and the Catmull-Rom latent
+ * forward pass (nt_forward).
+ *
+ * Contract (same as the reference unless stated):
+ *  - Every buffer is caller-owned device memory (hipMalloc or torch); the library never
+ *    allocates. Scratch space for the train step is passed in nt_params.workspace; its size
+ *    comes from nt_train_workspace_bytes().
+ *  - nt_train_step ACCUMULATES into the network and latent gradient buffers, which must
+ *    start at zero; nt_optimize_network / nt_optimize_latents consume the gradients and
+ *    re-zero them (train.cu:586, 621, 638).
+ *  - All work is enqueued on the given stream (a hipStream_t passed as void*, NULL = the
+ *    null stream) and is asynchronous; nothing synchronises.
+ *  - Errors are reported as nt_status codes, never as exceptions; nt_last_error() returns a
+ *    human-readable message for the last failing call on the calling thread. Argument
+ *    checking happens before anything is enqueued: a failing call enqueues nothing.
+ *  - Calls that share buffers must not overlap (the reference is not re-entrant either).
+ *
+ * Floating-point numbers use the reference's formats: fp32 latents, gradients and Adam
+ * moments; fp16 (IEEE binary16, passed as uint16_t bit patterns) network weights, biases
+ * and sampled features.
+ */
+#ifndef NT_NT_H
+#define NT_NT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NT_ABI_VERSION 1
+
+#define NT_MAX_GRIDS 4     /* NT_NUM_FEATURES (train.h:18) is the reference's fixed count */
+#define NT_MAX_MIPS 16
+#define NT_MAX_LAYERS 6    /* weight layers; the reference has NT_NUM_NETWORK_LAYERS = 3 */
+#define NT_MAX_TEXTURES 16 /* NT_MAX_REFERENCE_TEXTURES (train.h:19) */
+#define NT_MAX_OUTPUTS 16  /* NT_OUTPUT_SIZE (train.h:11) */
+#define NT_DEFAULT_REGION 512 /* kTrainingRegionSize (train.cu:827) */
+
+typedef enum nt_status {
+    NT_OK = 0,
+    NT_ERR_INVALID_ARGUMENT = 1, /* bad shape, count or enum value */
+    NT_ERR_NULL_POINTER = 2,     /* a required buffer pointer is NULL */
+    NT_ERR_MISALIGNED = 3,       /* a buffer is not aligned as documented */
+    NT_ERR_UNSUPPORTED = 4,      /* valid, but no kernel is built for this shape */
+    NT_ERR_WORKSPACE = 5,        /* workspace missing or smaller than required */
+    NT_ERR_HIP = 6               /* the HIP runtime reported an error (launch) */
+} nt_status;
+
+/* Mirrors TrainingKernelType (train.h:22-27). */
+typedef enum nt_kernel_type {
+    NT_UNCONSTRAINED = 0, /* float latents (train.cu:263-314, 460-509, 764-803) */
+    NT_BLOCK_FEATURES = 1, /* differentiable BC6 block latents (train.cu:316-458, 728-762) */
+    NT_FINALIZE = 2        /* BC6 latents, no latent gradient (train.cu:906-913) */
+} nt_kernel_type;
+
+/* Latent filter used when sampling the latent grids. */
+typedef enum nt_filter {
+    NT_FILTER_BILINEAR = 0,   /* trilinear over mips, fp16 accumulation (train.cu:263-314) */
+    NT_FILTER_CATMULL_ROM = 1 /* 16-tap Catmull-Rom on mip 0 (forward only, nt_forward) */
+} nt_filter;
+
+/* Mirrors AdamConstants (train.h:29-35). */
+typedef struct nt_adam {
+    float beta1;
+    float beta2;
+    float learning_rate;
+    float epsilon;
+} nt_adam;
+
+/*
+ * One latent grid (a reference `Feature`, train.h:51-67) with its mip chain.
+ *
+ * Unconstrained storage: all mips are flattened into one buffer per quantity. Mip m is
+ * max(width>>m,1) x max(height>>m,1) texels starting at texel mip_offset[m]; texel t of the
+ * buffer holds `channels` consecutive floats at [t*channels, (t+1)*channels). With
+ * channels = 3 this is exactly the reference's float3 row-major layout (train.cu:306).
+ *
+ * Block (BC6) storage, used by NT_BLOCK_FEATURES / NT_FINALIZE: mip m has
+ * max(w_m>>2,1) x max(h_m>>2,1) blocks starting at block block_offset[m]. A block record of
+ * block_params is (4*channels + 16) floats followed by two int32 (partition, mode): for
+ * channels = 3 it is the reference's 120-byte BC6Parameters (train.h:37-43). Gradient and
+ * moment records are (4*channels + 16) floats (BC6ParameterGradients, train.h:45-49).
+ */
+typedef struct nt_grid {
+    int width;
+    int height;
+    int num_mips;
+    int reserved0;
+    int64_t mip_offset[NT_MAX_MIPS];
+    float *values;
+    float *grads;
+    float *moment1;
+    float *moment2;
+    int64_t block_offset[NT_MAX_MIPS];
+    float *block_params;
+    float *block_grads;
+    float *block_moment1;
+    float *block_moment2;
+} nt_grid;
+
+typedef struct nt_latents {
+    int num_grids; /* 1..NT_MAX_GRIDS */
+    int channels;  /* per grid: 3, 4, 8 or 16 */
+    nt_grid grids[NT_MAX_GRIDS];
+} nt_latents;
+
+/*
+ * The tiny MLP (mlp.h). Layer l maps sizes[l] inputs to sizes[l+1] outputs; ReLU follows
+ * every layer but the last. Weights are fp16, column-major and padded to multiples of 16
+ * in both dimensions: W_l[col * AlignUp(sizes[l],16) + row], row = input, col = output
+ * (main.cpp:195, train.h:96-118); padding entries must be zero. Biases are sizes[l+1]
+ * fp16 values. Gradients and Adam moments are fp32 with the same layouts.
+ * used_outputs (<= sizes[num_layers]) is the reference's usedOutputChannels: the last
+ * layer's Adam update touches only its first used_outputs columns (train.cu:704-706).
+ */
+typedef struct nt_mlp {
+    int num_layers; /* 2..NT_MAX_LAYERS */
+    int sizes[NT_MAX_LAYERS + 1];
+    int used_outputs;
+    uint16_t *weights[NT_MAX_LAYERS];
+    float *weight_grads[NT_MAX_LAYERS];
+    float *weight_moment1[NT_MAX_LAYERS];
+    float *weight_moment2[NT_MAX_LAYERS];
+    uint16_t *biases[NT_MAX_LAYERS];
+    float *bias_grads[NT_MAX_LAYERS];
+    float *bias_moment1[NT_MAX_LAYERS];
+    float *bias_moment2[NT_MAX_LAYERS];
+} nt_mlp;
+
+/*
+ * A reference texture (train.h:69-77), in plain device memory instead of a CUDA texture
+ * object. texels holds the mip chain flattened like nt_grid: texel t of mip m is at
+ * [(mip_offset[m] + t) * pitch, ... + num_channels). pitch is 4 for 2..4 channels
+ * (the reference uploads 3-channel EXRs as float4, main.cpp:215-222) and 1 or 4 for one
+ * channel; addressing wraps (main.cpp:613-621).
+ */
+typedef struct nt_texture {
+    const float *texels;
+    int width;
+    int height;
+    int num_channels;
+    int num_mips;
+    int pitch;
+    float loss_weight;
+    int64_t mip_offset[NT_MAX_MIPS];
+} nt_texture;
+
+/*
+ * Everything one launch needs, mirroring KernelParams (train.h:120-157), passed by pointer.
+ */
+typedef struct nt_params {
+    nt_latents latents;
+    nt_mlp mlp;
+    nt_adam network_adam;
+    nt_adam feature_adam;
+    nt_texture textures[NT_MAX_TEXTURES];
+    int num_textures;
+
+    int image_width; /* sampling domain in texels (the reference textures' size) */
+    int image_height;
+    int texel_offset_x; /* training region origin (main.cpp:1043-1044) */
+    int texel_offset_y;
+    int region_width;   /* samples per region row; 0 means NT_DEFAULT_REGION */
+    int num_samples;    /* batch size; sample i sits at (i % region_width, i / region_width) */
+    int step;           /* Adam step; bias correction uses max(step, 1) (train.cu:528) */
+
+    float *inference_output;   /* nt_inference: [pixel][sizes[num_layers]] fp32 */
+    float *inference_mse_accum; /* nt_inference: SSE accumulator (one float) */
+
+    void *workspace; /* nt_train_step scratch, see nt_train_workspace_bytes */
+    size_t workspace_bytes;
+} nt_params;
+
+/* ---- layout helpers (host-only, no GPU needed) ------------------------------------- */
+
+int nt_abi_version(void);
+const char *nt_status_string(int status);
+/* Message for the last failing call on this thread ("" if none). */
+const char *nt_last_error(void);
+
+/* Fills mip_offset[0..num_mips) for a flattened mip chain and returns the total texel
+ * count (or -1 on a bad argument). Mip m has max(w>>m,1) x max(h>>m,1) texels. */
+int64_t nt_mip_chain_layout(int width, int height, int num_mips, int64_t *mip_offset);
+/* The same for 4x4 block storage (blocks per dimension = max(size>>2, 1), train.cu:220). */
+int64_t nt_block_chain_layout(int width, int height, int num_mips, int64_t *block_offset);
+/* Bytes of scratch nt_train_step needs for these parameters (0 on error). */
+size_t nt_train_workspace_bytes(const nt_params *params, nt_kernel_type type);
+
+/* ---- the hot path ----------------------------------------------------------------- */
+
+/*
+ * One fused training pass over params->num_samples samples (InvokeTraining,
+ * train.cu:1028-1048 -> TrainLoopPass :818-915): jittered sample position, latent sample,
+ * Catmull-Rom target, MLP forward, L2 loss gradient, MLP backward, latent gradient scatter.
+ * Accumulates into mlp.*_grads and the latent gradients.
+ */
+int nt_train_step(const nt_params *params, nt_kernel_type type, void *stream);
+
+/* Lazy Adam on the MLP (InvokeOptimizeNetwork, train.cu:985-988 -> :681-726). */
+int nt_optimize_network(const nt_params *params, void *stream);
+
+/* Lazy Adam on every texel (or block) of every grid and mip
+ * (InvokeOptimizeFeatures, train.cu:990-1026 -> :728-816). */
+int nt_optimize_latents(const nt_params *params, nt_kernel_type type, void *stream);
+
+/* Full-image inference at texel centres, mip 0 (InvokeInference, train.cu:1050-1062 ->
+ * :917-961): writes inference_output and adds the squared error to inference_mse_accum. */
+int nt_inference(const nt_params *params, void *stream);
+
+/*
+ * Tiny-MLP forward on given fp16 inputs (the ForwardPass* functions of mlp.h:18-99, as
+ * exercised by tests/forward_pass_test.cu). inputs: [count][sizes[0]] fp16;
+ * outputs: [count][sizes[num_layers]] fp16.
+ */
+int nt_mlp_forward(const nt_mlp *mlp, const uint16_t *inputs, uint16_t *outputs, int count,
+                   void *stream);
+
+/*
+ * Latent sample + MLP forward at caller-given coordinates. uvz: [count][3] fp32 (u, v, mip).
+ * filter selects bilinear/trilinear (train.cu:263-314) or 16-tap Catmull-Rom on mip 0.
+ * features (optional, may be NULL): [count][G*C] fp16 sampled features;
+ * outputs: [count][sizes[num_layers]] fp16.
+ */
+int nt_forward(const nt_latents *latents, const nt_mlp *mlp, nt_filter filter,
+               const float *uvz, int count, uint16_t *features, uint16_t *outputs,
+               void *stream);
+
+/* ---- the block codec -------------------------------------------------------------- */
+
+/*
+ * BC6H-style block codec for latent grids (no reference counterpart: the reference has no
+ * encoder). Each 4x4 texel block stores, per channel, two fp16 endpoints and sixteen 4-bit
+ * indices; a texel decodes to the fp16 whose order key is the BC6H 4-bit interpolation of
+ * the endpoint keys. Block record (channels multiple of 4): endpoints [channels][2] uint16,
+ * then for each of the 16 block pixels a channels*4-bit index word -> 12*channels bytes.
+ * Blocks per dimension = ceil(size / 4); texels outside the image are ignored.
+ */
+size_t nt_codec_block_bytes(int channels);
+size_t nt_codec_mip_chain_layout(int width, int height, int num_mips, int channels,
+                                 int64_t *byte_offset);
+/* values: [height*width][channels] fp32 (one mip); blocks: ceil(h/4)*ceil(w/4) records. */
+int nt_codec_encode(const float *values, int width, int height, int channels, void *blocks,
+                    void *stream);
+int nt_codec_decode(const void *blocks, int width, int height, int channels, float *values,
+                    void *stream);
+
+/* A grid quantized with the codec: mip m's blocks start at byte byte_offset[m]. */
+typedef struct nt_codec_grid {
+    int width;
+    int height;
+    int num_mips;
+    int reserved0;
+    int64_t byte_offset[NT_MAX_MIPS];
+    const void *blocks;
+} nt_codec_grid;
+
+typedef struct nt_decode_params {
+    int num_grids;
+    int channels; /* 16 (multiple of 4) */
+    nt_codec_grid grids[NT_MAX_GRIDS];
+    nt_mlp mlp;       /* weights and biases only */
+    int out_width;    /* output image size in pixels */
+    int out_height;
+    uint32_t seed;    /* per-pixel jitter / mip RNG seed */
+    float jitter;     /* jitter amplitude in output pixels (1 -> U[-0.5, 0.5)) */
+    float mip_min;    /* mip coordinate z ~ U[mip_min, mip_max) */
+    float mip_max;
+    uint16_t *output; /* [pixel][mlp.used_outputs] fp16 */
+} nt_decode_params;
+
+/*
+ * Decode a full image from codec-quantized latents: per pixel, jittered UV and random mip,
+ * trilinear sample of every grid, MLP forward, fp16 output.
+ */
+int nt_decode(const nt_decode_params *params, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NT_NT_H */

@@ -1,0 +1,168 @@
+// nt_adam.hip — lazy Adam as bandwidth-bound elementwise kernels (replaces
+// OptimizeNetwork / OptimizeFeatures, train.cu:521-816, 963-972).
+//
+// Semantics kept from the reference: a parameter whose gradient is exactly zero is skipped
+// (its moments do not decay), an updated parameter has its gradient re-zeroed, and the bias
+// corrections use t = max(step, 1) (train.cu:528, 580-586). The corrections 1 - beta^t are
+// computed once on the host and passed in. The latent kernel streams float4 gradient words
+// and touches the parameter and moments only where a gradient is non-zero.
+#include "nt_internal.hpp"
+
+namespace ntk {
+
+// AdamUpdateFloatParameter (train.cu:545-564), contraction as nvcc forms it.
+__device__ __forceinline__ float adam_update(float &m1, float &m2, float g, const AdamDesc &a, float w)
+{
+    m1 = fmaf(a.beta1, m1, (1.f - a.beta1) * g);
+    m2 = fmaf(a.beta2, m2, (1.f - a.beta2) * g * g);
+    const float mhat = m1 / a.bc1;
+    const float vhat = m2 / a.bc2;
+    return w - a.lr * mhat / (sqrtf(vhat) + a.eps);
+}
+
+__global__ __launch_bounds__(256) void net_adam_kernel(NetAdamDesc d)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= d.wstart[d.num_layers])
+        return;
+    int l = 0;
+    for (int k = 1; k < d.num_layers; ++k)
+        if (i >= d.wstart[k])
+            l = k;
+    const int local = i - d.wstart[l];
+    const int nw = d.rows[l] * d.cols[l];
+    if (local < nw) {
+        // OptimizePaddedParameterMatrix (train.cu:590-623): active rows x cols only.
+        const int row = local % d.rows[l], col = local / d.rows[l];
+        const int idx = col * d.pin[l] + row;
+        float *gp = d.g[l] + idx;
+        const float g = *gp;
+        if (g == 0.f)
+            return;
+        float m1 = d.m1[l][idx], m2 = d.m2[l][idx];
+        const float w = adam_update(m1, m2, g, d.a, h2f(d.w[l][idx]));
+        d.m1[l][idx] = m1;
+        d.m2[l][idx] = m2;
+        d.w[l][idx] = h_bits((_Float16)w);
+        *gp = 0.f;
+    } else {
+        // OptimizeParameterBuffer (train.cu:566-588).
+        const int idx = local - nw;
+        float *gp = d.bg[l] + idx;
+        const float g = *gp;
+        if (g == 0.f)
+            return;
+        float m1 = d.bm1[l][idx], m2 = d.bm2[l][idx];
+        const float w = adam_update(m1, m2, g, d.a, h2f(d.b[l][idx]));
+        d.bm1[l][idx] = m1;
+        d.bm2[l][idx] = m2;
+        d.b[l][idx] = h_bits((_Float16)w);
+        *gp = 0.f;
+    }
+}
+
+// Unconstrained latents: work item = 4 consecutive floats of one grid's flattened mip chain
+// (OptimizeUnconstrainedFeaturePass, train.cu:764-803).
+__global__ __launch_bounds__(256) void latent_adam_kernel(LatentAdamDesc d)
+{
+    const int64_t total = d.start[d.nseg];
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        int s = 0;
+#pragma unroll
+        for (int k = 1; k < NT_MAX_GRIDS; ++k)
+            if (k < d.nseg && i >= d.start[k])
+                s = k;
+        const int64_t f0 = (i - d.start[s]) * 4;
+        const int64_t rem = d.n[s] - f0;
+        float *g = d.g[s] + f0;
+        if (rem >= 4) {
+            float4 gv = *(const float4 *)g;
+            if (gv.x == 0.f && gv.y == 0.f && gv.z == 0.f && gv.w == 0.f)
+                continue;
+            float4 wv = *(const float4 *)(d.w[s] + f0);
+            float4 m1 = *(const float4 *)(d.m1[s] + f0);
+            float4 m2 = *(const float4 *)(d.m2[s] + f0);
+            if (gv.x != 0.f)
+                wv.x = adam_update(m1.x, m2.x, gv.x, d.a, wv.x);
+            if (gv.y != 0.f)
+                wv.y = adam_update(m1.y, m2.y, gv.y, d.a, wv.y);
+            if (gv.z != 0.f)
+                wv.z = adam_update(m1.z, m2.z, gv.z, d.a, wv.z);
+            if (gv.w != 0.f)
+                wv.w = adam_update(m1.w, m2.w, gv.w, d.a, wv.w);
+            *(float4 *)(d.w[s] + f0) = wv;
+            *(float4 *)(d.m1[s] + f0) = m1;
+            *(float4 *)(d.m2[s] + f0) = m2;
+            *(float4 *)g = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            for (int k = 0; k < rem; ++k) {
+                const float gs = g[k];
+                if (gs == 0.f)
+                    continue;
+                float m1 = d.m1[s][f0 + k], m2 = d.m2[s][f0 + k];
+                d.w[s][f0 + k] = adam_update(m1, m2, gs, d.a, d.w[s][f0 + k]);
+                d.m1[s][f0 + k] = m1;
+                d.m2[s][f0 + k] = m2;
+                g[k] = 0.f;
+            }
+        }
+    }
+}
+
+// BC6 block records (OptimizeFeatureBlock, train.cu:641-679): every float of the
+// parameter record except the trailing partition/mode pair.
+__global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
+{
+    const int64_t total = d.start[d.nseg];
+    const int rec = d.rec;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        int s = 0;
+#pragma unroll
+        for (int k = 1; k < NT_MAX_GRIDS; ++k)
+            if (k < d.nseg && i >= d.start[k])
+                s = k;
+        const int64_t b = i - d.start[s];
+        float *w = d.w[s] + b * (rec + 2);
+        float *g = d.g[s] + b * rec;
+        float *m1 = d.m1[s] + b * rec;
+        float *m2 = d.m2[s] + b * rec;
+        for (int k = 0; k < rec; ++k) {
+            const float gs = g[k];
+            if (gs == 0.f)
+                continue;
+            float a1 = m1[k], a2 = m2[k];
+            w[k] = adam_update(a1, a2, gs, d.a, w[k]);
+            m1[k] = a1;
+            m2[k] = a2;
+            g[k] = 0.f;
+        }
+    }
+}
+
+hipError_t launch_net_adam(const NetAdamDesc &d, hipStream_t s)
+{
+    const int n = d.wstart[d.num_layers];
+    if (n <= 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(net_adam_kernel, dim3((n + 255) / 256), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_latent_adam(const LatentAdamDesc &d, hipStream_t s)
+{
+    const int64_t n = d.start[d.nseg];
+    if (n <= 0)
+        return hipSuccess;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 8192)
+        blocks = 8192;
+    if (d.rec > 0)
+        hipLaunchKernelGGL(block_adam_kernel, dim3((unsigned)blocks), dim3(256), 0, s, d);
+    else
+        hipLaunchKernelGGL(latent_adam_kernel, dim3((unsigned)blocks), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
+} // namespace ntk

@@ -1,0 +1,748 @@
+// nt_api.cpp — the extern "C" boundary declared in include/nt/nt.h.
+//
+// Every entry point validates its arguments completely before enqueueing anything, turns
+// the caller's structs into compact kernel descriptors and dispatches to a gfx950 kernel
+// instantiated for the network shape. Nothing here allocates device memory.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "nt_internal.hpp"
+
+using namespace ntk;
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int status, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int ok()
+{
+    g_error[0] = '\0';
+    return NT_OK;
+}
+
+int hip_status(hipError_t e, const char *what)
+{
+    if (e != hipSuccess)
+        return fail(NT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+constexpr int pad16(int x) { return (x + 15) & ~15; }
+
+int mip_dim_h(int size, int mip)
+{
+    int d = size >> mip;
+    return d > 0 ? d : 1;
+}
+
+// Shape of the MLP -> kernel instantiation (see ShapeId). Returns -1 if none is built.
+int mlp_shape(const nt_mlp *m)
+{
+    const int L = m->num_layers;
+    if (L < 2 || L > NT_MAX_LAYERS)
+        return -1;
+    for (int l = 0; l <= L; ++l)
+        if (m->sizes[l] < 1)
+            return -1;
+    if (m->sizes[L] > NT_MAX_OUTPUTS)
+        return -1;
+    const int k0 = pad16(m->sizes[0]);
+    const int h = pad16(m->sizes[1]);
+    for (int l = 1; l < L; ++l)
+        if (pad16(m->sizes[l]) != h)
+            return -1;
+    const int nh = L - 1;
+    if (k0 == 16 && h == 32 && nh == 2)
+        return kShapeRef;
+    if (k0 == 16 && h == 16 && nh == 1)
+        return kShapeFpt;
+    if (k0 == 16 && h == 64 && nh == 2)
+        return kShapeC1;
+    if (k0 == 32 && h == 64 && nh == 2)
+        return kShapeC2;
+    if (k0 == 64 && h == 64 && nh == 3)
+        return kShapeC4;
+    return -1;
+}
+
+int shape_channels(int shape)
+{
+    switch (shape) {
+    case kShapeRef:
+        return 3;
+    case kShapeC1:
+        return 8;
+    case kShapeC2:
+    case kShapeC4:
+        return 16;
+    default:
+        return 0;
+    }
+}
+
+const char *shape_list()
+{
+    return "12(16)->32->32->16 C=3; 12(16)->16->16; 8(16)->64->64->16 C=8; 32->64->64->16 C=16; "
+           "64->64->64->64->16 C=16";
+}
+
+int check_mlp(const nt_mlp *m, bool need_grads, bool need_moments, int *shape)
+{
+    if (!m)
+        return fail(NT_ERR_NULL_POINTER, "mlp is NULL");
+    *shape = mlp_shape(m);
+    if (*shape < 0)
+        return fail(NT_ERR_UNSUPPORTED, "no kernel is built for this MLP shape (built: %s)", shape_list());
+    if (m->used_outputs < 0 || m->used_outputs > m->sizes[m->num_layers])
+        return fail(NT_ERR_INVALID_ARGUMENT, "used_outputs %d outside [0, %d]", m->used_outputs,
+                    m->sizes[m->num_layers]);
+    for (int l = 0; l < m->num_layers; ++l) {
+        if (!m->weights[l] || !m->biases[l])
+            return fail(NT_ERR_NULL_POINTER, "layer %d weights/biases are NULL", l);
+        if (need_grads && (!m->weight_grads[l] || !m->bias_grads[l]))
+            return fail(NT_ERR_NULL_POINTER, "layer %d gradient buffers are NULL", l);
+        if (need_moments && (!m->weight_moment1[l] || !m->weight_moment2[l] ||
+                             !m->bias_moment1[l] || !m->bias_moment2[l]))
+            return fail(NT_ERR_NULL_POINTER, "layer %d Adam moment buffers are NULL", l);
+    }
+    return NT_OK;
+}
+
+MlpDesc mlp_desc(const nt_mlp *m)
+{
+    MlpDesc d{};
+    d.num_layers = m->num_layers;
+    for (int l = 0; l < m->num_layers; ++l) {
+        d.W[l] = m->weights[l];
+        d.B[l] = m->biases[l];
+    }
+    for (int l = 0; l <= m->num_layers; ++l)
+        d.sizes[l] = m->sizes[l];
+    return d;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Validates the latent grids for sampling. unconstrained: values (+ grads) needed;
+// otherwise block records.
+int check_latents(const nt_latents *lat, int shape, bool need_grads, bool blocks)
+{
+    if (!lat)
+        return fail(NT_ERR_NULL_POINTER, "latents is NULL");
+    if (lat->num_grids < 1 || lat->num_grids > NT_MAX_GRIDS)
+        return fail(NT_ERR_INVALID_ARGUMENT, "num_grids %d outside [1, %d]", lat->num_grids, NT_MAX_GRIDS);
+    const int C = shape_channels(shape);
+    if (lat->channels != C)
+        return fail(NT_ERR_UNSUPPORTED, "this MLP shape is built for %d channels per grid, got %d", C,
+                    lat->channels);
+    for (int gi = 0; gi < lat->num_grids; ++gi) {
+        const nt_grid &g = lat->grids[gi];
+        if (g.width < 1 || g.height < 1 || g.num_mips < 1 || g.num_mips > NT_MAX_MIPS)
+            return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: bad size %dx%d or mip count %d", gi, g.width,
+                        g.height, g.num_mips);
+        if (!blocks) {
+            if (!g.values || (need_grads && !g.grads))
+                return fail(NT_ERR_NULL_POINTER, "grid %d: values/grads are NULL", gi);
+            if ((C % 4 == 0) && !aligned16(g.values))
+                return fail(NT_ERR_MISALIGNED, "grid %d: values must be 16-byte aligned", gi);
+            for (int m = 0; m < g.num_mips; ++m)
+                if (g.mip_offset[m] < 0 || ((C % 4 == 0) && (g.mip_offset[m] * C) % 4))
+                    return fail(NT_ERR_MISALIGNED, "grid %d: bad mip_offset[%d]", gi, m);
+        } else {
+            if (!g.block_params || (need_grads && !g.block_grads))
+                return fail(NT_ERR_NULL_POINTER, "grid %d: block_params/block_grads are NULL", gi);
+            if ((g.width & 3) && g.width > 4)
+                return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: block storage needs a width multiple of 4", gi);
+            if ((g.height & 3) && g.height > 4)
+                return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: block storage needs a height multiple of 4", gi);
+        }
+    }
+    return NT_OK;
+}
+
+GridDesc grid_desc(const nt_grid &g, int C)
+{
+    GridDesc d{};
+    d.values = g.values;
+    d.grads = g.grads;
+    d.block_params = g.block_params;
+    d.block_grads = g.block_grads;
+    d.w = g.width;
+    d.h = g.height;
+    d.num_mips = g.num_mips;
+    for (int m = 0; m < NT_MAX_MIPS; ++m) {
+        d.mip_off[m] = g.mip_offset[m];
+        d.block_off[m] = g.block_offset[m];
+    }
+    (void)C;
+    return d;
+}
+
+// Output-channel packing of the reference textures (train.cu:105-157,
+// main.cpp:243-258). Returns the number of packed channels or a negative status.
+int pack_targets(const nt_texture *tex, int ntex, int8_t *out_tex, int8_t *out_ch, float *out_w,
+                 TexDesc *td)
+{
+    for (int o = 0; o < NT_MAX_OUTPUTS; ++o) {
+        out_tex[o] = -1;
+        out_ch[o] = 0;
+        out_w[o] = 1.f;
+    }
+    if (ntex < 0 || ntex > NT_MAX_TEXTURES)
+        return -fail(NT_ERR_INVALID_ARGUMENT, "num_textures %d outside [0, %d]", ntex, NT_MAX_TEXTURES);
+    int oc = 0;
+    for (int ti = 0; ti < ntex && oc < NT_MAX_OUTPUTS; ++ti) {
+        const nt_texture &t = tex[ti];
+        td[ti] = TexDesc{};
+        if (!t.texels || t.num_channels <= 0)
+            continue;
+        if (t.width < 1 || t.height < 1 || t.num_mips < 1 || t.num_mips > NT_MAX_MIPS)
+            return -fail(NT_ERR_INVALID_ARGUMENT, "texture %d: bad size or mip count", ti);
+        const int nc = t.num_channels == 1 ? 1 : (t.num_channels < 4 ? t.num_channels : 4);
+        if (!((t.pitch == 4) || (t.pitch == 1 && nc == 1)))
+            return -fail(NT_ERR_INVALID_ARGUMENT, "texture %d: pitch must be 4 (or 1 for one channel)", ti);
+        if (t.pitch == 4 && !aligned16(t.texels + t.mip_offset[0] * 4))
+            return -fail(NT_ERR_MISALIGNED, "texture %d: texels must be 16-byte aligned", ti);
+        td[ti].texels = t.texels + t.mip_offset[0] * t.pitch;
+        td[ti].w = t.width;
+        td[ti].h = t.height;
+        td[ti].pitch = t.pitch;
+        td[ti].nch = nc;
+        for (int c = 0; c < nc && oc < NT_MAX_OUTPUTS; ++c, ++oc) {
+            out_tex[oc] = (int8_t)ti;
+            out_ch[oc] = (int8_t)c;
+            out_w[oc] = t.loss_weight;
+        }
+    }
+    return oc;
+}
+
+struct TrainPlan {
+    int shape, nwg, chunks_per_wg, tiles_x, P, stage1_blocks, rows_per_block;
+    int fp_floats;
+    int fp_w[NT_MAX_GRIDS], fp_h[NT_MAX_GRIDS], fp_off[NT_MAX_GRIDS];
+    size_t lds, workspace;
+};
+
+constexpr size_t kMaxLds = 160 * 1024;
+
+int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
+{
+    if (!p)
+        return fail(NT_ERR_NULL_POINTER, "params is NULL");
+    if (type != NT_UNCONSTRAINED && type != NT_BLOCK_FEATURES && type != NT_FINALIZE)
+        return fail(NT_ERR_INVALID_ARGUMENT, "bad kernel type %d", (int)type);
+    int shape;
+    int st = check_mlp(&p->mlp, true, false, &shape);
+    if (st)
+        return st;
+    if (shape != kShapeRef && shape != kShapeC2 && shape != kShapeC4)
+        return fail(NT_ERR_UNSUPPORTED, "training is built for 12->32->32->16 (C=3), 32->64->64->16 "
+                                        "(C=16) and 64->64->64->64->16 (C=16)");
+    st = check_latents(&p->latents, shape, type != NT_FINALIZE, type != NT_UNCONSTRAINED);
+    if (st)
+        return st;
+    if (p->latents.num_grids * p->latents.channels != p->mlp.sizes[0])
+        return fail(NT_ERR_INVALID_ARGUMENT, "MLP input %d != num_grids*channels %d", p->mlp.sizes[0],
+                    p->latents.num_grids * p->latents.channels);
+    if (p->image_width < 1 || p->image_height < 1)
+        return fail(NT_ERR_INVALID_ARGUMENT, "image size %dx%d", p->image_width, p->image_height);
+    if (p->num_samples < 1)
+        return fail(NT_ERR_INVALID_ARGUMENT, "num_samples %d", p->num_samples);
+    const int rw = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
+    const int rows = (int)(((int64_t)p->num_samples + rw - 1) / rw);
+    plan->shape = shape;
+    plan->chunks_per_wg = 4;
+    const int tile_w = kChunkW * plan->chunks_per_wg;
+    plan->tiles_x = (rw + tile_w - 1) / tile_w;
+    const int tiles_y = (rows + kChunkH - 1) / kChunkH;
+    if ((int64_t)plan->tiles_x * tiles_y > (1 << 30))
+        return fail(NT_ERR_INVALID_ARGUMENT, "too many samples");
+    plan->nwg = plan->tiles_x * tiles_y;
+    plan->P = train_grad_total(shape);
+    plan->rows_per_block = 32;
+    plan->stage1_blocks = (plan->nwg + plan->rows_per_block - 1) / plan->rows_per_block;
+    plan->workspace = ((size_t)plan->nwg + (size_t)plan->stage1_blocks) * (size_t)plan->P * sizeof(float);
+
+    // LDS footprint box per grid: every texel a 64 x 8 block of positions can touch.
+    const int C = p->latents.channels;
+    size_t lds = train_lds_static(shape);
+    int fp = 0;
+    for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+        const nt_grid &g = p->latents.grids[gi];
+        plan->fp_w[gi] = (int)std::ceil((double)tile_w * g.width / p->image_width) + 5;
+        plan->fp_h[gi] = (int)std::ceil((double)kChunkH * g.height / p->image_height) + 5;
+        plan->fp_off[gi] = fp;
+        fp += plan->fp_w[gi] * plan->fp_h[gi] * C;
+    }
+    plan->fp_floats = fp;
+    if (type != NT_UNCONSTRAINED || lds + (size_t)fp * 4 > kMaxLds)
+        plan->fp_floats = 0; // scatter straight to global memory
+    plan->lds = lds + (size_t)plan->fp_floats * 4;
+    return NT_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int nt_abi_version(void) { return NT_ABI_VERSION; }
+
+const char *nt_status_string(int status)
+{
+    switch (status) {
+    case NT_OK:
+        return "ok";
+    case NT_ERR_INVALID_ARGUMENT:
+        return "invalid argument";
+    case NT_ERR_NULL_POINTER:
+        return "null pointer";
+    case NT_ERR_MISALIGNED:
+        return "misaligned buffer";
+    case NT_ERR_UNSUPPORTED:
+        return "unsupported shape";
+    case NT_ERR_WORKSPACE:
+        return "workspace too small";
+    case NT_ERR_HIP:
+        return "HIP runtime error";
+    default:
+        return "unknown status";
+    }
+}
+
+const char *nt_last_error(void) { return g_error; }
+
+int64_t nt_mip_chain_layout(int width, int height, int num_mips, int64_t *mip_offset)
+{
+    if (width < 1 || height < 1 || num_mips < 1 || num_mips > NT_MAX_MIPS || !mip_offset)
+        return -1;
+    int64_t off = 0;
+    for (int m = 0; m < NT_MAX_MIPS; ++m) {
+        mip_offset[m] = m < num_mips ? off : 0;
+        if (m < num_mips)
+            off += (int64_t)mip_dim_h(width, m) * mip_dim_h(height, m);
+    }
+    return off;
+}
+
+int64_t nt_block_chain_layout(int width, int height, int num_mips, int64_t *block_offset)
+{
+    if (width < 1 || height < 1 || num_mips < 1 || num_mips > NT_MAX_MIPS || !block_offset)
+        return -1;
+    int64_t off = 0;
+    for (int m = 0; m < NT_MAX_MIPS; ++m) {
+        block_offset[m] = m < num_mips ? off : 0;
+        if (m < num_mips) {
+            const int bw = mip_dim_h(width, m) >> 2, bh = mip_dim_h(height, m) >> 2;
+            off += (int64_t)(bw > 0 ? bw : 1) * (bh > 0 ? bh : 1);
+        }
+    }
+    return off;
+}
+
+size_t nt_train_workspace_bytes(const nt_params *params, nt_kernel_type type)
+{
+    TrainPlan plan;
+    if (plan_train(params, type, &plan) != NT_OK)
+        return 0;
+    return plan.workspace;
+}
+
+int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
+{
+    TrainPlan plan;
+    int st = plan_train(p, type, &plan);
+    if (st)
+        return st;
+    if (!p->workspace || p->workspace_bytes < plan.workspace)
+        return fail(NT_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", plan.workspace,
+                    p->workspace ? p->workspace_bytes : (size_t)0);
+    if (!aligned16(p->workspace))
+        return fail(NT_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+
+    TrainDesc d{};
+    d.mlp = mlp_desc(&p->mlp);
+    const int C = p->latents.channels;
+    for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+        const nt_grid &g = p->latents.grids[gi];
+        d.grid[gi] = grid_desc(g, C);
+        if (g.values)
+            d.grid[gi].values = g.values + g.mip_offset[0] * C;
+        if (g.grads)
+            d.grid[gi].grads = g.grads + g.mip_offset[0] * C;
+        d.grid[gi].fp_w = plan.fp_w[gi];
+        d.grid[gi].fp_h = plan.fp_h[gi];
+        d.grid[gi].fp_off = plan.fp_off[gi];
+    }
+    const int nout = pack_targets(p->textures, p->num_textures, d.out_tex, d.out_ch, d.out_w, d.tex);
+    if (nout < 0)
+        return -nout;
+    d.ntex = p->num_textures;
+    d.G = p->latents.num_grids;
+    d.C = C;
+    d.image_w = p->image_width;
+    d.image_h = p->image_height;
+    d.off_x = p->texel_offset_x;
+    d.off_y = p->texel_offset_y;
+    d.region_w = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
+    d.num_samples = p->num_samples;
+    d.step = (uint32_t)p->step;
+    d.tiles_x = plan.tiles_x;
+    d.chunks_per_wg = plan.chunks_per_wg;
+    d.fp_floats = plan.fp_floats;
+    d.partial = (float *)p->workspace;
+
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = launch_train(plan.shape, type, d, plan.nwg, plan.lds, s);
+    if (e != hipSuccess)
+        return hip_status(e, "train kernel launch");
+
+    ReduceDesc r{};
+    r.partial = d.partial;
+    r.tmp = d.partial + (size_t)plan.nwg * plan.P;
+    r.rows = plan.nwg;
+    r.rows_per_block = plan.rows_per_block;
+    r.P = plan.P;
+    r.stage1_blocks = plan.stage1_blocks;
+    r.num_layers = p->mlp.num_layers;
+    int off = 0;
+    for (int l = 0; l < p->mlp.num_layers; ++l) {
+        r.off[l] = off;
+        r.kin[l] = pad16(p->mlp.sizes[l]);
+        r.kout[l] = pad16(p->mlp.sizes[l + 1]);
+        r.nbias[l] = p->mlp.sizes[l + 1];
+        r.wgrad[l] = p->mlp.weight_grads[l];
+        r.bgrad[l] = p->mlp.bias_grads[l];
+        off += r.kin[l] * r.kout[l] + r.kout[l];
+    }
+    e = launch_reduce(r, s);
+    if (e != hipSuccess)
+        return hip_status(e, "gradient reduction launch");
+    return ok();
+}
+
+static AdamDesc adam_desc(const nt_adam &a, int step)
+{
+    AdamDesc d;
+    const int t = step > 0 ? step : 1;
+    d.beta1 = a.beta1;
+    d.beta2 = a.beta2;
+    d.lr = a.learning_rate;
+    d.eps = a.epsilon;
+    d.bc1 = 1.f - powf(a.beta1, (float)t);
+    d.bc2 = 1.f - powf(a.beta2, (float)t);
+    return d;
+}
+
+int nt_optimize_network(const nt_params *p, void *stream)
+{
+    if (!p)
+        return fail(NT_ERR_NULL_POINTER, "params is NULL");
+    int shape;
+    int st = check_mlp(&p->mlp, true, true, &shape);
+    if (st)
+        return st;
+    const nt_mlp &m = p->mlp;
+    NetAdamDesc d{};
+    d.a = adam_desc(p->network_adam, p->step);
+    d.num_layers = m.num_layers;
+    int n = 0;
+    for (int l = 0; l < m.num_layers; ++l) {
+        d.rows[l] = m.sizes[l];
+        d.cols[l] = l == m.num_layers - 1 ? m.used_outputs : m.sizes[l + 1];
+        d.pin[l] = pad16(m.sizes[l]);
+        d.nbias[l] = m.sizes[l + 1];
+        d.wstart[l] = n;
+        n += d.rows[l] * d.cols[l] + d.nbias[l];
+        d.w[l] = m.weights[l];
+        d.g[l] = m.weight_grads[l];
+        d.m1[l] = m.weight_moment1[l];
+        d.m2[l] = m.weight_moment2[l];
+        d.b[l] = m.biases[l];
+        d.bg[l] = m.bias_grads[l];
+        d.bm1[l] = m.bias_moment1[l];
+        d.bm2[l] = m.bias_moment2[l];
+    }
+    d.wstart[m.num_layers] = n;
+    return hip_status(launch_net_adam(d, (hipStream_t)stream), "network Adam launch");
+}
+
+int nt_optimize_latents(const nt_params *p, nt_kernel_type type, void *stream)
+{
+    if (!p)
+        return fail(NT_ERR_NULL_POINTER, "params is NULL");
+    if (type != NT_UNCONSTRAINED && type != NT_BLOCK_FEATURES && type != NT_FINALIZE)
+        return fail(NT_ERR_INVALID_ARGUMENT, "bad kernel type %d", (int)type);
+    const nt_latents &lat = p->latents;
+    if (lat.num_grids < 1 || lat.num_grids > NT_MAX_GRIDS)
+        return fail(NT_ERR_INVALID_ARGUMENT, "num_grids %d", lat.num_grids);
+    if (lat.channels < 1 || lat.channels > 16)
+        return fail(NT_ERR_INVALID_ARGUMENT, "channels %d", lat.channels);
+    const int C = lat.channels;
+    const bool blocks = type != NT_UNCONSTRAINED; // FINALIZE optimizes blocks too (train.cu:1018-1025)
+    LatentAdamDesc d{};
+    d.a = adam_desc(p->feature_adam, p->step);
+    d.nseg = lat.num_grids;
+    d.rec = blocks ? 4 * C + 16 : 0;
+    int64_t start = 0;
+    for (int gi = 0; gi < lat.num_grids; ++gi) {
+        const nt_grid &g = lat.grids[gi];
+        if (g.width < 1 || g.height < 1 || g.num_mips < 1 || g.num_mips > NT_MAX_MIPS)
+            return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: bad size or mip count", gi);
+        d.start[gi] = start;
+        if (!blocks) {
+            // The mips must be stored back to back from mip_offset[0].
+            int64_t texels = 0;
+            for (int m = 0; m < g.num_mips; ++m) {
+                if (g.mip_offset[m] != g.mip_offset[0] + texels)
+                    return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: mips are not contiguous", gi);
+                texels += (int64_t)mip_dim_h(g.width, m) * mip_dim_h(g.height, m);
+            }
+            if (!g.values || !g.grads || !g.moment1 || !g.moment2)
+                return fail(NT_ERR_NULL_POINTER, "grid %d: values/grads/moments are NULL", gi);
+            const int64_t base = g.mip_offset[0] * C;
+            if (!aligned16(g.values + base) || !aligned16(g.grads + base) || !aligned16(g.moment1 + base) ||
+                !aligned16(g.moment2 + base))
+                return fail(NT_ERR_MISALIGNED, "grid %d: latent buffers must be 16-byte aligned", gi);
+            d.w[gi] = g.values + base;
+            d.g[gi] = g.grads + base;
+            d.m1[gi] = g.moment1 + base;
+            d.m2[gi] = g.moment2 + base;
+            d.n[gi] = texels * C;
+            start += (d.n[gi] + 3) / 4;
+        } else {
+            int64_t nb = 0;
+            for (int m = 0; m < g.num_mips; ++m) {
+                if (g.block_offset[m] != g.block_offset[0] + nb)
+                    return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: block mips are not contiguous", gi);
+                const int bw = mip_dim_h(g.width, m) >> 2, bh = mip_dim_h(g.height, m) >> 2;
+                nb += (int64_t)(bw > 0 ? bw : 1) * (bh > 0 ? bh : 1);
+            }
+            if (!g.block_params || !g.block_grads || !g.block_moment1 || !g.block_moment2)
+                return fail(NT_ERR_NULL_POINTER, "grid %d: block buffers are NULL", gi);
+            d.w[gi] = g.block_params + g.block_offset[0] * (4 * C + 18);
+            d.g[gi] = g.block_grads + g.block_offset[0] * (4 * C + 16);
+            d.m1[gi] = g.block_moment1 + g.block_offset[0] * (4 * C + 16);
+            d.m2[gi] = g.block_moment2 + g.block_offset[0] * (4 * C + 16);
+            d.n[gi] = nb;
+            start += nb;
+        }
+    }
+    d.start[lat.num_grids] = start;
+    return hip_status(launch_latent_adam(d, (hipStream_t)stream), "latent Adam launch");
+}
+
+static int fwd_common(const nt_latents *lat, const nt_mlp *mlp, bool need_latents, FwdDesc *d,
+                      int *shape)
+{
+    int st = check_mlp(mlp, false, false, shape);
+    if (st)
+        return st;
+    *d = FwdDesc{};
+    d->mlp = mlp_desc(mlp);
+    if (need_latents) {
+        st = check_latents(lat, *shape, false, false);
+        if (st)
+            return st;
+        if (lat->num_grids * lat->channels != mlp->sizes[0])
+            return fail(NT_ERR_INVALID_ARGUMENT, "MLP input %d != num_grids*channels %d", mlp->sizes[0],
+                        lat->num_grids * lat->channels);
+        d->G = lat->num_grids;
+        d->C = lat->channels;
+        for (int gi = 0; gi < lat->num_grids; ++gi)
+            d->grid[gi] = grid_desc(lat->grids[gi], lat->channels);
+    }
+    return NT_OK;
+}
+
+int nt_inference(const nt_params *p, void *stream)
+{
+    if (!p)
+        return fail(NT_ERR_NULL_POINTER, "params is NULL");
+    if (!p->inference_output || !p->inference_mse_accum)
+        return fail(NT_ERR_NULL_POINTER, "inference_output / inference_mse_accum are NULL");
+    if (p->image_width < 1 || p->image_height < 1)
+        return fail(NT_ERR_INVALID_ARGUMENT, "image size %dx%d", p->image_width, p->image_height);
+    if ((int64_t)p->image_width * p->image_height > (1ll << 31) - 64)
+        return fail(NT_ERR_INVALID_ARGUMENT, "image too large");
+    FwdDesc d;
+    int shape;
+    int st = fwd_common(&p->latents, &p->mlp, true, &d, &shape);
+    if (st)
+        return st;
+    float dummy_w[NT_MAX_OUTPUTS];
+    const int nout = pack_targets(p->textures, p->num_textures, d.out_tex, d.out_ch, dummy_w, d.tex);
+    if (nout < 0)
+        return -nout;
+    d.ntex = p->num_textures;
+    d.count = p->image_width * p->image_height;
+    d.image_w = p->image_width;
+    d.image_h = p->image_height;
+    d.out32 = p->inference_output;
+    d.sse = p->inference_mse_accum;
+    d.out_stride = p->mlp.sizes[p->mlp.num_layers];
+    return hip_status(launch_forward(shape, kFwdInference, d, (hipStream_t)stream), "inference launch");
+}
+
+int nt_mlp_forward(const nt_mlp *mlp, const uint16_t *inputs, uint16_t *outputs, int count, void *stream)
+{
+    if (!inputs || !outputs)
+        return fail(NT_ERR_NULL_POINTER, "inputs/outputs are NULL");
+    if (count < 0)
+        return fail(NT_ERR_INVALID_ARGUMENT, "count %d", count);
+    FwdDesc d;
+    int shape;
+    int st = fwd_common(nullptr, mlp, false, &d, &shape);
+    if (st)
+        return st;
+    if (count == 0)
+        return ok();
+    d.count = count;
+    d.inputs = inputs;
+    d.out16 = outputs;
+    d.out_stride = mlp->sizes[mlp->num_layers];
+    return hip_status(launch_forward(shape, kFwdMlp, d, (hipStream_t)stream), "MLP forward launch");
+}
+
+int nt_forward(const nt_latents *latents, const nt_mlp *mlp, nt_filter filter, const float *uvz, int count,
+               uint16_t *features, uint16_t *outputs, void *stream)
+{
+    if (!uvz || !outputs)
+        return fail(NT_ERR_NULL_POINTER, "uvz/outputs are NULL");
+    if (count < 0)
+        return fail(NT_ERR_INVALID_ARGUMENT, "count %d", count);
+    if (filter != NT_FILTER_BILINEAR && filter != NT_FILTER_CATMULL_ROM)
+        return fail(NT_ERR_INVALID_ARGUMENT, "bad filter %d", (int)filter);
+    FwdDesc d;
+    int shape;
+    int st = fwd_common(latents, mlp, true, &d, &shape);
+    if (st)
+        return st;
+    if (count == 0)
+        return ok();
+    d.count = count;
+    d.uvz = uvz;
+    d.features = features;
+    d.out16 = outputs;
+    d.out_stride = mlp->sizes[mlp->num_layers];
+    const int mode = filter == NT_FILTER_BILINEAR ? kFwdBilinear : kFwdCatmullRom;
+    return hip_status(launch_forward(shape, mode, d, (hipStream_t)stream), "forward launch");
+}
+
+size_t nt_codec_block_bytes(int channels)
+{
+    if (channels < 4 || channels > 16 || channels % 4)
+        return 0;
+    return (size_t)12 * channels;
+}
+
+size_t nt_codec_mip_chain_layout(int width, int height, int num_mips, int channels, int64_t *byte_offset)
+{
+    const size_t rec = nt_codec_block_bytes(channels);
+    if (!rec || width < 1 || height < 1 || num_mips < 1 || num_mips > NT_MAX_MIPS || !byte_offset)
+        return 0;
+    size_t off = 0;
+    for (int m = 0; m < NT_MAX_MIPS; ++m) {
+        byte_offset[m] = m < num_mips ? (int64_t)off : 0;
+        if (m < num_mips) {
+            const int w = mip_dim_h(width, m), h = mip_dim_h(height, m);
+            off += (size_t)((w + 3) / 4) * ((h + 3) / 4) * rec;
+        }
+    }
+    return off;
+}
+
+int nt_codec_encode(const float *values, int width, int height, int channels, void *blocks, void *stream)
+{
+    if (!values || !blocks)
+        return fail(NT_ERR_NULL_POINTER, "values/blocks are NULL");
+    if (width < 1 || height < 1 || !nt_codec_block_bytes(channels))
+        return fail(NT_ERR_INVALID_ARGUMENT, "size %dx%d, channels %d (need 4, 8, 12 or 16)", width, height,
+                    channels);
+    if (((uintptr_t)blocks & 3u) || ((uintptr_t)values & 3u))
+        return fail(NT_ERR_MISALIGNED, "values/blocks must be 4-byte aligned");
+    return hip_status(launch_codec_encode(values, width, height, channels, (uint8_t *)blocks, (hipStream_t)stream),
+                      "codec encode launch");
+}
+
+int nt_codec_decode(const void *blocks, int width, int height, int channels, float *values, void *stream)
+{
+    if (!values || !blocks)
+        return fail(NT_ERR_NULL_POINTER, "values/blocks are NULL");
+    if (width < 1 || height < 1 || !nt_codec_block_bytes(channels))
+        return fail(NT_ERR_INVALID_ARGUMENT, "size %dx%d, channels %d (need 4, 8, 12 or 16)", width, height,
+                    channels);
+    if (!aligned16(blocks) || !aligned16(values))
+        return fail(NT_ERR_MISALIGNED, "values/blocks must be 16-byte aligned");
+    return hip_status(
+        launch_codec_decode((const uint8_t *)blocks, width, height, channels, values, (hipStream_t)stream),
+        "codec decode launch");
+}
+
+int nt_decode(const nt_decode_params *p, void *stream)
+{
+    if (!p)
+        return fail(NT_ERR_NULL_POINTER, "params is NULL");
+    if (!p->output)
+        return fail(NT_ERR_NULL_POINTER, "output is NULL");
+    if (p->out_width < 1 || p->out_height < 1 || (int64_t)p->out_width * p->out_height > (1ll << 31) - 64)
+        return fail(NT_ERR_INVALID_ARGUMENT, "output size %dx%d", p->out_width, p->out_height);
+    FwdDesc d;
+    int shape;
+    int st = fwd_common(nullptr, &p->mlp, false, &d, &shape);
+    if (st)
+        return st;
+    const int C = shape_channels(shape);
+    if (C != 16 && C != 8)
+        return fail(NT_ERR_UNSUPPORTED, "decode is built for 8 or 16 channels per grid");
+    if (p->channels != C)
+        return fail(NT_ERR_UNSUPPORTED, "this MLP shape decodes %d channels per grid, got %d", C, p->channels);
+    if (p->num_grids < 1 || p->num_grids > NT_MAX_GRIDS || p->num_grids * p->channels != p->mlp.sizes[0])
+        return fail(NT_ERR_INVALID_ARGUMENT, "num_grids %d x channels %d != MLP input %d", p->num_grids,
+                    p->channels, p->mlp.sizes[0]);
+    if (p->mlp.used_outputs < 1)
+        return fail(NT_ERR_INVALID_ARGUMENT, "used_outputs must be >= 1");
+    for (int gi = 0; gi < p->num_grids; ++gi) {
+        const nt_codec_grid &g = p->grids[gi];
+        if (!g.blocks)
+            return fail(NT_ERR_NULL_POINTER, "grid %d blocks are NULL", gi);
+        if (g.width < 1 || g.height < 1 || g.num_mips < 1 || g.num_mips > NT_MAX_MIPS)
+            return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: bad size or mip count", gi);
+        for (int m = 0; m < g.num_mips; ++m)
+            if (!aligned16((const uint8_t *)g.blocks + g.byte_offset[m]))
+                return fail(NT_ERR_MISALIGNED, "grid %d mip %d blocks must be 16-byte aligned", gi, m);
+        d.cgrid[gi].blocks = (const uint8_t *)g.blocks;
+        d.cgrid[gi].w = g.width;
+        d.cgrid[gi].h = g.height;
+        d.cgrid[gi].num_mips = g.num_mips;
+        for (int m = 0; m < NT_MAX_MIPS; ++m)
+            d.cgrid[gi].byte_off[m] = g.byte_offset[m];
+    }
+    d.G = p->num_grids;
+    d.C = p->channels;
+    d.count = p->out_width * p->out_height;
+    d.image_w = p->out_width;
+    d.image_h = p->out_height;
+    d.out16 = p->output;
+    d.out_stride = p->mlp.used_outputs;
+    d.seed = p->seed;
+    d.jitter = p->jitter;
+    d.mip_min = p->mip_min;
+    d.mip_max = p->mip_max;
+    return hip_status(launch_forward(shape, kFwdDecode, d, (hipStream_t)stream), "decode launch");
+}
+
+} // extern "C"

@@ -1,0 +1,156 @@
+// nt_codec.hip — BC6H-style latent block codec (the reference has no encoder; its BC6
+// decode emulation is train.cu:159-202). Per 4x4 block and channel: two fp16 endpoints
+// (stored as order keys) and sixteen 4-bit indices into the BC6H interpolation weights.
+//
+// Encode: one thread per (block, channel). Endpoints are the min and max order key of the
+// block's fp16-rounded values; each index minimises |v - decode(i)| in fp32 (lowest index
+// wins ties). Integer key arithmetic plus IEEE fp32 compares make the result bit-exact
+// against the CPU restatement. Decode: one thread per (texel, 4 channels), float4 stores.
+#include "nt_internal.hpp"
+
+namespace ntk {
+
+template <int C>
+__global__ __launch_bounds__(256) void codec_encode_kernel(const float *values, int W, int H,
+                                                           uint8_t *blocks)
+{
+    constexpr int BPW = 256 / C; // blocks per workgroup pass
+    __shared__ uint8_t nib[BPW][16 * C];
+    const int tid = threadIdx.x, lb = tid / C, c = tid % C;
+    const int bw = (W + 3) >> 2, bh = (H + 3) >> 2;
+    const int64_t nblocks = (int64_t)bw * bh;
+    for (int64_t base = (int64_t)blockIdx.x * BPW; base < nblocks; base += (int64_t)gridDim.x * BPW) {
+        const int64_t b = base + lb;
+        const bool active = lb < BPW && b < nblocks; // C = 12 leaves 256 % 12 threads idle
+        uint8_t *rec = blocks + b * (12 * C);
+        if (active) {
+            const int bx = (int)(b % bw), by = (int)(b / bw);
+            float v[16];
+            uint32_t kmin = 0xFFFFu, kmax = 0u;
+#pragma unroll
+            for (int p = 0; p < 16; ++p) {
+                const int x = 4 * bx + (p & 3), y = 4 * by + (p >> 2);
+                v[p] = 0.f;
+                if (x < W && y < H) {
+                    const float raw = values[((int64_t)y * W + x) * C + c];
+                    v[p] = fminf(fmaxf(raw, -65504.f), 65504.f);
+                    const uint32_t k = codec_key(h_bits((_Float16)v[p]));
+                    kmin = k < kmin ? k : kmin;
+                    kmax = k > kmax ? k : kmax;
+                }
+            }
+            *(uint32_t *)(rec + 4 * c) = kmin | (kmax << 16);
+#pragma unroll
+            for (int p = 0; p < 16; ++p) {
+                const int x = 4 * bx + (p & 3), y = 4 * by + (p >> 2);
+                int best = 0;
+                if (x < W && y < H) {
+                    float best_err = __builtin_inff();
+                    for (int i = 0; i < 16; ++i) {
+                        const float err = fabsf(v[p] - codec_value(kmin, kmax, i));
+                        if (err < best_err) {
+                            best_err = err;
+                            best = i;
+                        }
+                    }
+                }
+                nib[lb][p * C + c] = (uint8_t)best;
+            }
+        }
+        __syncthreads();
+        if (active) {
+            // Index area: nibble p*C + c; word w packs nibbles 8w .. 8w+7, low nibble first.
+            for (int w = c; w < 2 * C; w += C) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    word |= (uint32_t)nib[lb][8 * w + t] << (4 * t);
+                *(uint32_t *)(rec + 4 * C + 4 * w) = word;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int C>
+__global__ __launch_bounds__(256) void codec_decode_kernel(const uint8_t *blocks, int W, int H,
+                                                           float *values)
+{
+    constexpr int G4 = C / 4;
+    const int bw = (W + 3) >> 2;
+    const int64_t total = (int64_t)W * H * G4;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        const int64_t texel = i / G4;
+        const int cg = (int)(i % G4);
+        const int x = (int)(texel % W), y = (int)(texel / W);
+        const uint8_t *rec = blocks + ((int64_t)(y >> 2) * bw + (x >> 2)) * (12 * C);
+        const int pix = ((y & 3) << 2) + (x & 3);
+        const uint4 e = *(const uint4 *)(rec + 16 * cg);
+        const uint32_t idx = *(const uint16_t *)(rec + 4 * C + pix * (C / 2) + 2 * cg);
+        float4 out;
+        out.x = codec_value(e.x & 0xFFFFu, e.x >> 16, idx & 15);
+        out.y = codec_value(e.y & 0xFFFFu, e.y >> 16, (idx >> 4) & 15);
+        out.z = codec_value(e.z & 0xFFFFu, e.z >> 16, (idx >> 8) & 15);
+        out.w = codec_value(e.w & 0xFFFFu, e.w >> 16, (idx >> 12) & 15);
+        *(float4 *)(values + texel * C + 4 * cg) = out;
+    }
+}
+
+template <int C>
+static hipError_t encode_c(const float *values, int w, int h, uint8_t *blocks, hipStream_t s)
+{
+    const int64_t nblocks = (int64_t)((w + 3) / 4) * ((h + 3) / 4);
+    int64_t groups = (nblocks + 256 / C - 1) / (256 / C);
+    if (groups > 65536)
+        groups = 65536;
+    hipLaunchKernelGGL(codec_encode_kernel<C>, dim3((unsigned)groups), dim3(256), 0, s, values, w, h,
+                       blocks);
+    return hipGetLastError();
+}
+
+template <int C>
+static hipError_t decode_c(const uint8_t *blocks, int w, int h, float *values, hipStream_t s)
+{
+    const int64_t total = (int64_t)w * h * (C / 4);
+    int64_t groups = (total + 255) / 256;
+    if (groups > 65536)
+        groups = 65536;
+    hipLaunchKernelGGL(codec_decode_kernel<C>, dim3((unsigned)groups), dim3(256), 0, s, blocks, w, h,
+                       values);
+    return hipGetLastError();
+}
+
+hipError_t launch_codec_encode(const float *values, int w, int h, int C, uint8_t *blocks, hipStream_t s)
+{
+    switch (C) {
+    case 4:
+        return encode_c<4>(values, w, h, blocks, s);
+    case 8:
+        return encode_c<8>(values, w, h, blocks, s);
+    case 12:
+        return encode_c<12>(values, w, h, blocks, s);
+    case 16:
+        return encode_c<16>(values, w, h, blocks, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_codec_decode(const uint8_t *blocks, int w, int h, int C, float *values, hipStream_t s)
+{
+    switch (C) {
+    case 4:
+        return decode_c<4>(blocks, w, h, values, s);
+    case 8:
+        return decode_c<8>(blocks, w, h, values, s);
+    case 12:
+        return decode_c<12>(blocks, w, h, values, s);
+    case 16:
+        return decode_c<16>(blocks, w, h, values, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+} // namespace ntk

@@ -1,0 +1,184 @@
+// nt_device.hpp — device helpers shared by the gfx950 kernels.
+//
+// Numeric policy: every kernel is compiled with -ffp-contract=off; a fused multiply-add
+// appears only as an explicit fmaf(), at the places where nvcc's default contraction
+// fuses the reference's CUDA source. fp16 conversions (v_cvt_f16_f32) round to nearest
+// even and keep subnormals; fp16 adds (v_add_f16) are correctly rounded, like __hadd.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ntk {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// D(32x32,f32) += A(32x16,f16) * B(16x32,f16) on one wave64. Lane l holds
+// A[l%32][8*(l/32)+i], B[8*(l/32)+i][l%32] (i=0..7) and D[8*j+4*(l/32)+r][l%32] in
+// element 4*j+r (j,r=0..3).
+__device__ __forceinline__ f16v mfma32(h8 a, h8 b, f16v c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)bits_h(b); }
+
+// xorshift32 and the per-sample seed (train.cu:37-58, 833).
+__device__ __forceinline__ uint32_t xorshift32(uint32_t &s)
+{
+    uint32_t x = s;
+    x ^= x << 13;
+    x ^= x >> 17;
+    x ^= x << 5;
+    s = x;
+    return x;
+}
+__device__ __forceinline__ float uniform01(uint32_t &s)
+{
+    return (float)(xorshift32(s) & 0x00FFFFFFu) * (1.0f / 16777216.0f);
+}
+__device__ __forceinline__ uint32_t mix_seed(uint32_t index, uint32_t step)
+{
+    const uint32_t s = index ^ (step * 747796405u + 2891336453u);
+    return s ? s : 1u;
+}
+
+__device__ __forceinline__ float clampf(float x, float lo, float hi)
+{
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+// WrapTexelCoord (train.cu:65-69).
+__device__ __forceinline__ int wrap_coord(int c, int size)
+{
+    int w = c % size;
+    return w < 0 ? w + size : w;
+}
+__device__ __forceinline__ int mip_dim(int size, int mip)
+{
+    int d = size >> mip;
+    return d > 0 ? d : 1;
+}
+
+// Bilinear footprint of one mip level (train.cu:284-303): unwrapped origin texel and the
+// four corner weights (corner = cx + 2*cy), each already scaled by the mip weight.
+struct Footprint {
+    int x0, y0;
+    float w[4];
+};
+__device__ __forceinline__ Footprint bilinear_footprint(float u, float v, int w, int h,
+                                                        float mip_weight)
+{
+    Footprint f;
+    const float tu = fmaf(u, (float)w, -0.5f);
+    const float tv = fmaf(v, (float)h, -0.5f);
+    const float bu = floorf(tu), bv = floorf(tv);
+    f.x0 = (int)bu;
+    f.y0 = (int)bv;
+    const float fx = tu - bu, fy = tv - bv;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float wu = (c & 1) ? fx : 1.f - fx;
+        const float wv = (c >> 1) ? fy : 1.f - fy;
+        f.w[c] = mip_weight * (wu * wv);
+    }
+    return f;
+}
+
+// Catmull-Rom weights (filter/catmull_rom.h:56-59, contraction explicit).
+__device__ __forceinline__ void cr_weights(float f, float w[4])
+{
+    w[0] = f * fmaf(f, fmaf(f, -0.5f, 1.0f), -0.5f);
+    w[1] = fmaf(f * f, fmaf(f, 1.5f, -2.5f), 1.0f);
+    w[2] = f * fmaf(f, fmaf(f, -1.5f, 2.0f), 0.5f);
+    w[3] = (f * f) * fmaf(f, 0.5f, -0.5f);
+}
+// Tap origin (first of four taps) and weights along one axis (catmull_rom.h:43-59).
+__device__ __forceinline__ int cr_axis(float uv, int size, float w[4])
+{
+    const float s = uv * (float)size;
+    const float b = floorf(s - 0.5f);
+    cr_weights(s - (b + 0.5f), w);
+    return (int)b - 1;
+}
+
+// ---- BC6 emulation (train.cu:19-35, 159-202) ---------------------------------------
+__device__ __forceinline__ float bc6_unquantize(float e, int bits)
+{
+    return ldexpf(fmaf(31744.f, e, 32768.f), -bits);
+}
+__device__ __forceinline__ float bc6_y(float q0, float q1, float x)
+{
+    return fmaf(ldexpf(q1 - q0, 3), x, q0);
+}
+__device__ __forceinline__ int bc6_hy(float y)
+{
+    return (int)fmaxf(floorf((y - 1.f) / 1024.f) - 1.f, 0.f);
+}
+__device__ __forceinline__ float bc6_decompress(float e0, float e1, int bits, float x)
+{
+    const float y = bc6_y(bc6_unquantize(e0, bits), bc6_unquantize(e1, bits), x);
+    const int hy = bc6_hy(y);
+    return ldexpf(y / 1024.f - (float)hy, hy - 14);
+}
+__device__ __forceinline__ int bc6_partition_mask(int p)
+{
+    // gBC6HPartitionSets (train.cu:20-29): the standard BC6H/BC7 two-subset masks.
+    constexpr int kSets[32] = {
+        0xCCCC, 0x8888, 0xEEEE, 0xECC8, 0xC880, 0xFEEC, 0xFEC8, 0xEC80,
+        0xC800, 0xFFEC, 0xFE80, 0xE800, 0xFFE8, 0xFF00, 0xFFF0, 0xF000,
+        0xF710, 0x008E, 0x7100, 0x08CE, 0x008C, 0x7310, 0x3100, 0x8CCE,
+        0x088C, 0x3110, 0x6666, 0x366C, 0x17E8, 0x0FF0, 0x718E, 0x399C,
+    };
+    return kSets[p & 31];
+}
+__device__ __forceinline__ int bc6_mode_bits(int m)
+{
+    constexpr int kBits[10] = {10, 7, 11, 11, 11, 9, 8, 8, 8, 6}; // train.cu:31-34
+    return kBits[(unsigned)m < 10u ? m : 0];
+}
+
+// ---- block codec (no reference counterpart) ----------------------------------------
+// Order key: a monotone map of fp16 bit patterns to uint16 (negative values reversed).
+__device__ __forceinline__ uint32_t codec_key(uint32_t h)
+{
+    return (h & 0x8000u) ? (~h & 0xFFFFu) : (h | 0x8000u);
+}
+__device__ __forceinline__ uint32_t codec_unkey(uint32_t k)
+{
+    return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu);
+}
+// BC6H 4-bit interpolation weights {0,4,9,13,17,21,26,30,34,38,43,47,51,55,60,64}.
+__device__ __forceinline__ int codec_weight(int i)
+{
+    // packed 6 bits per entry would also do; a switch-free table in registers:
+    constexpr int kW[16] = {0, 4, 9, 13, 17, 21, 26, 30, 34, 38, 43, 47, 51, 55, 60, 64};
+    return kW[i & 15];
+}
+__device__ __forceinline__ uint32_t codec_interp(uint32_t k0, uint32_t k1, int i)
+{
+    const uint32_t w = (uint32_t)codec_weight(i);
+    return (k0 * (64u - w) + k1 * w + 32u) >> 6;
+}
+__device__ __forceinline__ float codec_value(uint32_t k0, uint32_t k1, int i)
+{
+    return h2f((uint16_t)codec_unkey(codec_interp(k0, k1, i)));
+}
+
+// ---- atomics -----------------------------------------------------------------------
+// Hardware float add on global memory (global_atomic_add_f32, no return).
+__device__ __forceinline__ void global_add(float *p, float v)
+{
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// LDS float add (ds_add_f32).
+__device__ __forceinline__ void lds_add(float *p, float v)
+{
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+} // namespace ntk

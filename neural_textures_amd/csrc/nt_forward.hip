@@ -1,0 +1,415 @@
+// nt_forward.hip — forward-only passes on gfx950: the tiny-MLP forward
+// (mlp.h:18-99, the path tests/forward_pass_test.cu exercises), latent sample + MLP at
+// given coordinates, full-image inference (train.cu:917-961) and decode from
+// codec-quantized latents.
+//
+// Each wave runs 32-sample MFMA tiles in a grid-stride loop; forward weight fragments are
+// staged in LDS once per workgroup. Lane group g of sample c (lane = 32g + c) gathers the
+// network-input features 16q + 8g + e and ends with output rows o = chained_feature(0,g,e).
+#include "nt_internal.hpp"
+
+namespace ntk {
+
+constexpr int kFwdThreads = 256;
+
+template <class S>
+struct FwdLayout {
+    static constexpr int frag_bytes = S::fwd_total() * kWave * 16;
+    static constexpr int bias_off = frag_bytes;
+    static constexpr int bytes = frag_bytes + ((S::bias_total() * 4 + 15) / 16) * 16;
+};
+
+// Mip pair for mip coordinate z (train.cu:266-281).
+__device__ __forceinline__ int mip_pair(int num_mips, float z, int (&mips)[2], float (&w)[2])
+{
+    const float fz = floorf(z);
+    const int base = (int)fz;
+    const float frac = z - fz;
+    const int max_mip = num_mips > 0 ? num_mips - 1 : 0;
+    const int n = frac > 0.f ? 2 : 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        int m = base + i < max_mip ? base + i : max_mip;
+        mips[i] = m < 0 ? 0 : m;
+        w[i] = i ? frac : 1.f - frac;
+    }
+    return n;
+}
+
+// Trilinear unconstrained latent sample of the lane's natural-layout features
+// (train.cu:263-314): fp16 rounding of every corner contribution, fp16 accumulation.
+template <int C, int KQ>
+__device__ __forceinline__ void sample_bilinear(const FwdDesc &d, float u, float v, float z, int g,
+                                                h8 (&x)[KQ])
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[q][e] = (_Float16)0.f;
+        if constexpr (C == 16 || C == 8) {
+            const int gi = C == 16 ? q : 2 * q + g;
+            if (gi >= d.G)
+                continue;
+            const GridDesc &gr = d.grid[C == 16 ? q : (g ? ((2 * q + 1) & 3) : 2 * q)];
+            const int cb = C == 16 ? 8 * g : 0;
+            int mips[2];
+            float mw[2];
+            const int nm = mip_pair(gr.num_mips, z, mips, mw);
+            for (int mi = 0; mi < nm; ++mi) {
+                const int w = mip_dim(gr.w, mips[mi]), h = mip_dim(gr.h, mips[mi]);
+                const Footprint f = bilinear_footprint(u, v, w, h, mw[mi]);
+                const float *vals = gr.values + gr.mip_off[mips[mi]] * C + cb;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int tx = wrap_coord(f.x0 + (c & 1), w), ty = wrap_coord(f.y0 + (c >> 1), h);
+                    const float4 *p = (const float4 *)(vals + ((int64_t)ty * w + tx) * C);
+                    const float4 a = p[0], b = p[1];
+                    const float wc = f.w[c];
+                    x[q][0] = x[q][0] + (_Float16)(wc * a.x);
+                    x[q][1] = x[q][1] + (_Float16)(wc * a.y);
+                    x[q][2] = x[q][2] + (_Float16)(wc * a.z);
+                    x[q][3] = x[q][3] + (_Float16)(wc * a.w);
+                    x[q][4] = x[q][4] + (_Float16)(wc * b.x);
+                    x[q][5] = x[q][5] + (_Float16)(wc * b.y);
+                    x[q][6] = x[q][6] + (_Float16)(wc * b.z);
+                    x[q][7] = x[q][7] + (_Float16)(wc * b.w);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int feat = 16 * q + 8 * g + e;
+                if (feat >= d.G * C)
+                    continue;
+                const GridDesc &gr = d.grid[feat / C];
+                const int ch = feat % C;
+                int mips[2];
+                float mw[2];
+                const int nm = mip_pair(gr.num_mips, z, mips, mw);
+                _Float16 a = (_Float16)0.f;
+                for (int mi = 0; mi < nm; ++mi) {
+                    const int w = mip_dim(gr.w, mips[mi]), h = mip_dim(gr.h, mips[mi]);
+                    const Footprint f = bilinear_footprint(u, v, w, h, mw[mi]);
+                    const float *vals = gr.values + gr.mip_off[mips[mi]] * C;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int tx = wrap_coord(f.x0 + (c & 1), w), ty = wrap_coord(f.y0 + (c >> 1), h);
+                        a = a + (_Float16)(f.w[c] * vals[((int64_t)ty * w + tx) * C + ch]);
+                    }
+                }
+                x[q][e] = a;
+            }
+        }
+    }
+}
+
+// 16-tap Catmull-Rom latent sample on mip 0: fp32 accumulation, one fp16 rounding.
+template <int C, int KQ>
+__device__ __forceinline__ void sample_catmull_rom(const FwdDesc &d, float u, float v, int g,
+                                                   h8 (&x)[KQ])
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            acc[e] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int feat = 16 * q + 8 * g + e;
+            if (feat >= d.G * C)
+                continue;
+            const GridDesc &gr = d.grid[feat / C];
+            const int ch = feat % C;
+            float wx[4], wy[4];
+            const int x0 = cr_axis(u, gr.w, wx);
+            const int y0 = cr_axis(v, gr.h, wy);
+            const float *vals = gr.values + gr.mip_off[0] * C;
+            for (int j = 0; j < 4; ++j) {
+                const int ty = wrap_coord(y0 + j, gr.h);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tx = wrap_coord(x0 + i, gr.w);
+                    acc[e] = fmaf(vals[((int64_t)ty * gr.w + tx) * C + ch], wx[i] * wy[j], acc[e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[q][e] = (_Float16)acc[e];
+    }
+}
+
+// Trilinear sample of codec-quantized latents (C multiple of 8 per lane group).
+template <int C, int KQ>
+__device__ __forceinline__ void sample_codec(const FwdDesc &d, float u, float v, float z, int g,
+                                             h8 (&x)[KQ])
+{
+    static_assert(C == 16 || C == 8, "codec decode expects 8 or 16 channels");
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[q][e] = (_Float16)0.f;
+        const int gi = C == 16 ? q : 2 * q + g;
+        if (gi >= d.G)
+            continue;
+        const CodecGrid &gr = d.cgrid[C == 16 ? q : (g ? ((2 * q + 1) & 3) : 2 * q)];
+        const int cb = C == 16 ? 8 * g : 0;
+        int mips[2];
+        float mw[2];
+        const int nm = mip_pair(gr.num_mips, z, mips, mw);
+        for (int mi = 0; mi < nm; ++mi) {
+            const int w = mip_dim(gr.w, mips[mi]), h = mip_dim(gr.h, mips[mi]);
+            const int bw = (w + 3) >> 2;
+            const Footprint f = bilinear_footprint(u, v, w, h, mw[mi]);
+            const uint8_t *base = gr.blocks + gr.byte_off[mips[mi]];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int tx = wrap_coord(f.x0 + (c & 1), w), ty = wrap_coord(f.y0 + (c >> 1), h);
+                const uint8_t *rec = base + ((int64_t)(ty >> 2) * bw + (tx >> 2)) * (12 * C);
+                const int pix = ((ty & 3) << 2) + (tx & 3);
+                const uint4 e01 = *(const uint4 *)(rec + 4 * cb);
+                const uint4 e23 = *(const uint4 *)(rec + 4 * cb + 16);
+                const uint32_t idx = *(const uint32_t *)(rec + 4 * C + pix * (C / 2) + cb / 2);
+                const uint32_t ends[8] = {e01.x, e01.y, e01.z, e01.w, e23.x, e23.y, e23.z, e23.w};
+                const float wc = f.w[c];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float val = codec_value(ends[e] & 0xFFFFu, ends[e] >> 16, (idx >> (4 * e)) & 15);
+                    x[q][e] = x[q][e] + (_Float16)(wc * val);
+                }
+            }
+        }
+    }
+}
+
+template <class S, int C, int MODE>
+__global__ __launch_bounds__(kFwdThreads) void forward_kernel(FwdDesc d)
+{
+    using LY = FwdLayout<S>;
+    constexpr int L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
+    extern __shared__ __align__(16) unsigned char smem[];
+    h8 *frags = (h8 *)smem;
+    float *bias = (float *)(smem + LY::bias_off);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
+    stage_weights<S, true>(d.mlp, frags, bias, tid, kFwdThreads);
+    __syncthreads();
+
+    float sse = 0.f;
+    const int ntiles = (d.count + 31) / 32;
+    for (int tile = blockIdx.x * 4 + wave; tile < ntiles; tile += gridDim.x * 4) {
+        const int s = tile * 32 + c;
+        const bool valid = s < d.count;
+        h8 x0[KQ0];
+        float u = 0.f, v = 0.f;
+        if constexpr (MODE == kFwdMlp) {
+            const int in = d.mlp.sizes[0];
+#pragma unroll
+            for (int q = 0; q < KQ0; ++q)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int feat = natural_feature(q, g, e);
+                    x0[q][e] = (valid && feat < in) ? bits_h(d.inputs[(int64_t)s * in + feat])
+                                                    : (_Float16)0.f;
+                }
+        } else if constexpr (MODE == kFwdBilinear || MODE == kFwdCatmullRom) {
+            const int sc = valid ? s : 0;
+            u = d.uvz[3 * (int64_t)sc];
+            v = d.uvz[3 * (int64_t)sc + 1];
+            const float z = d.uvz[3 * (int64_t)sc + 2];
+            if constexpr (MODE == kFwdBilinear)
+                sample_bilinear<C, KQ0>(d, u, v, z, g, x0);
+            else
+                sample_catmull_rom<C, KQ0>(d, u, v, g, x0);
+        } else if constexpr (MODE == kFwdInference) {
+            const int sc = valid ? s : 0;
+            const int px = sc % d.image_w, py = sc / d.image_w;
+            u = ((float)px + 0.5f) / (float)d.image_w; // train.cu:926-933
+            v = ((float)py + 0.5f) / (float)d.image_h;
+            sample_bilinear<C, KQ0>(d, u, v, 0.f, g, x0);
+        } else { // kFwdDecode
+            const int sc = valid ? s : 0;
+            const int px = sc % d.image_w, py = sc / d.image_w;
+            uint32_t st = mix_seed((uint32_t)sc, d.seed);
+            const float jx = uniform01(st) - 0.5f;
+            const float jy = uniform01(st) - 0.5f;
+            const float zu = uniform01(st);
+            const float posx = clampf(fmaf(d.jitter, jx, (float)px + 0.5f), 0.5f, (float)d.image_w - 0.5f);
+            const float posy = clampf(fmaf(d.jitter, jy, (float)py + 0.5f), 0.5f, (float)d.image_h - 0.5f);
+            u = posx / (float)d.image_w;
+            v = posy / (float)d.image_h;
+            const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
+            sample_codec<C, KQ0>(d, u, v, z, g, x0);
+        }
+        if (d.features != nullptr && valid) {
+            const int nf = d.G * C;
+#pragma unroll
+            for (int q = 0; q < KQ0; ++q)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int feat = natural_feature(q, g, e);
+                    if (feat < nf)
+                        d.features[(int64_t)s * nf + feat] = h_bits(x0[q][e]);
+                }
+        }
+
+        // MLP forward (mlp.h:65-99)
+        h8 xh[HQ];
+        {
+            f16v acc[HA];
+            layer_forward<KQ0, HA>(frags + S::fwd_off(0) * kWave, bias + S::bias_off(0), x0, acc, lane);
+            to_fragments<HQ, HA, true>(acc, xh);
+#pragma unroll
+            for (int l = 1; l < NH; ++l) {
+                layer_forward<HQ, HA>(frags + S::fwd_off(l) * kWave, bias + S::bias_off(l), xh, acc, lane);
+                to_fragments<HQ, HA, true>(acc, xh);
+            }
+        }
+        f16v out[1];
+        layer_forward<HQ, 1>(frags + S::fwd_off(L - 1) * kWave, bias + S::bias_off(L - 1), xh, out, lane);
+
+        if (!valid)
+            continue;
+        if constexpr (MODE == kFwdInference) {
+            // Targets for the SSE (train.cu:935-960).
+            float tgt[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                tgt[e] = 0.f;
+            for (int ti = 0; ti < d.ntex; ++ti) {
+                bool need = false;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    need |= d.out_tex[chained_feature(0, g, e)] == ti;
+                if (!need)
+                    continue;
+                const TexDesc tx = d.tex[ti];
+                float wx[4], wy[4];
+                const int x0t = cr_axis(u, tx.w, wx), y0t = cr_axis(v, tx.h, wy);
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+                for (int j = 0; j < 4; ++j) {
+                    const int y = wrap_coord(y0t + j, tx.h);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int x = wrap_coord(x0t + i, tx.w);
+                        const float wxy = wx[i] * wy[j];
+                        const int64_t base = ((int64_t)y * tx.w + x) * tx.pitch;
+                        if (tx.pitch == 4) {
+                            const float4 p = *(const float4 *)(tx.texels + base);
+                            acc[0] = fmaf(p.x, wxy, acc[0]);
+                            if (tx.nch > 1)
+                                acc[1] = fmaf(p.y, wxy, acc[1]);
+                            if (tx.nch > 2)
+                                acc[2] = fmaf(p.z, wxy, acc[2]);
+                            if (tx.nch > 3)
+                                acc[3] = fmaf(p.w, wxy, acc[3]);
+                        } else {
+                            acc[0] = fmaf(tx.texels[base], wxy, acc[0]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int o = chained_feature(0, g, e);
+                    if (d.out_tex[o] == ti) {
+                        const int ch = d.out_ch[o];
+                        tgt[e] = ch == 0 ? acc[0] : ch == 1 ? acc[1] : ch == 2 ? acc[2] : acc[3];
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int o = chained_feature(0, g, e);
+                if (o < d.out_stride) {
+                    const float y = (float)(_Float16)out[0][e];
+                    d.out32[(int64_t)s * d.out_stride + o] = y;
+                    const float err = y - tgt[e];
+                    sse = fmaf(err, err, sse);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int o = chained_feature(0, g, e);
+                if (o < d.out_stride)
+                    d.out16[(int64_t)s * d.out_stride + o] = h_bits((_Float16)out[0][e]);
+            }
+        }
+    }
+    if constexpr (MODE == kFwdInference) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1)
+            sse += __shfl_xor(sse, off);
+        if (lane == 0 && sse != 0.f)
+            global_add(d.sse, sse);
+    }
+}
+
+template <class S, int C, int MODE>
+static hipError_t launch_fwd(const FwdDesc &d, hipStream_t s)
+{
+    const int ntiles = (d.count + 31) / 32;
+    int blocks = (ntiles + 3) / 4;
+    if (blocks > 2048)
+        blocks = 2048;
+    if (blocks < 1)
+        blocks = 1;
+    hipLaunchKernelGGL((forward_kernel<S, C, MODE>), dim3(blocks), dim3(kFwdThreads),
+                       FwdLayout<S>::bytes, s, d);
+    return hipGetLastError();
+}
+
+template <class S, int C>
+static hipError_t launch_modes(int mode, const FwdDesc &d, hipStream_t s)
+{
+    switch (mode) {
+    case kFwdBilinear:
+        return launch_fwd<S, C, kFwdBilinear>(d, s);
+    case kFwdCatmullRom:
+        return launch_fwd<S, C, kFwdCatmullRom>(d, s);
+    case kFwdInference:
+        return launch_fwd<S, C, kFwdInference>(d, s);
+    case kFwdDecode:
+        if constexpr (C == 16 || C == 8)
+            return launch_fwd<S, C, kFwdDecode>(d, s);
+        return hipErrorInvalidValue;
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_forward(int shape, int mode, const FwdDesc &d, hipStream_t s)
+{
+    if (mode == kFwdMlp) {
+        switch (shape) {
+        case kShapeRef:
+            return launch_fwd<Shape<16, 32, 2>, 0, kFwdMlp>(d, s);
+        case kShapeFpt:
+            return launch_fwd<Shape<16, 16, 1>, 0, kFwdMlp>(d, s);
+        case kShapeC1:
+            return launch_fwd<Shape<16, 64, 2>, 0, kFwdMlp>(d, s);
+        case kShapeC2:
+            return launch_fwd<Shape<32, 64, 2>, 0, kFwdMlp>(d, s);
+        case kShapeC4:
+            return launch_fwd<Shape<64, 64, 3>, 0, kFwdMlp>(d, s);
+        default:
+            return hipErrorInvalidValue;
+        }
+    }
+    switch (shape) {
+    case kShapeRef:
+        return launch_modes<Shape<16, 32, 2>, 3>(mode, d, s);
+    case kShapeC1:
+        return launch_modes<Shape<16, 64, 2>, 8>(mode, d, s);
+    case kShapeC2:
+        return launch_modes<Shape<32, 64, 2>, 16>(mode, d, s);
+    case kShapeC4:
+        return launch_modes<Shape<64, 64, 3>, 16>(mode, d, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+} // namespace ntk

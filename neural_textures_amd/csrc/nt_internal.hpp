@@ -1,0 +1,145 @@
+// nt_internal.hpp — launch descriptors passed by value to the gfx950 kernels, and the
+// internal launcher entry points the C ABI (nt_api.cpp) dispatches to. Descriptors carry
+// only what a kernel reads, so kernel arguments stay small.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nt/nt.h"
+#include "nt_mlp.hpp"
+
+namespace ntk {
+
+// Samples per workgroup chunk in the train kernel: a 16 x 8 block of region positions,
+// four waves of 32 samples (one 32-sample MFMA tile per wave).
+constexpr int kChunkW = 16;
+constexpr int kChunkH = 8;
+constexpr int kChunk = kChunkW * kChunkH;
+constexpr int kTrainThreads = 256;
+constexpr int kRowStride = kChunk + 8; // fp16 row stride of the LDS transposes
+
+// One latent grid at the mip levels a kernel samples.
+struct GridDesc {
+    const float *values;
+    float *grads;
+    const float *block_params;
+    float *block_grads;
+    int w, h, num_mips;
+    int fp_w, fp_h, fp_off; // train kernel: LDS footprint box and offset (floats)
+    int64_t mip_off[NT_MAX_MIPS];   // texels
+    int64_t block_off[NT_MAX_MIPS]; // blocks
+};
+
+struct TexDesc {
+    const float *texels; // mip 0
+    int w, h, pitch, nch;
+};
+
+// Everything the fused train kernel reads.
+struct TrainDesc {
+    MlpDesc mlp;
+    GridDesc grid[NT_MAX_GRIDS];
+    TexDesc tex[NT_MAX_TEXTURES];
+    int8_t out_tex[NT_MAX_OUTPUTS]; // texture feeding each output channel, -1 = none
+    int8_t out_ch[NT_MAX_OUTPUTS];
+    float out_w[NT_MAX_OUTPUTS]; // per-channel loss weight (train.cu:105-157)
+    int G, C, ntex;
+    int image_w, image_h, off_x, off_y, region_w, num_samples;
+    uint32_t step;
+    int tiles_x, chunks_per_wg;
+    int fp_floats; // LDS footprint floats (0: scatter straight to global)
+    float *partial; // [gridDim.x][grad_total] per-workgroup MLP gradient partials
+};
+
+// Gradient reduction descriptor: partial[rows][P] -> mlp gradients.
+struct ReduceDesc {
+    const float *partial;
+    float *tmp;
+    int rows, rows_per_block, P, stage1_blocks;
+    int num_layers;
+    int off[NT_MAX_LAYERS], kin[NT_MAX_LAYERS], kout[NT_MAX_LAYERS], nbias[NT_MAX_LAYERS];
+    float *wgrad[NT_MAX_LAYERS];
+    float *bgrad[NT_MAX_LAYERS];
+};
+
+enum FwdMode { kFwdMlp = 0, kFwdBilinear = 1, kFwdCatmullRom = 2, kFwdInference = 3, kFwdDecode = 4 };
+
+struct CodecGrid {
+    const uint8_t *blocks;
+    int w, h, num_mips;
+    int64_t byte_off[NT_MAX_MIPS];
+};
+
+// Forward-only passes: nt_mlp_forward, nt_forward, nt_inference, nt_decode.
+struct FwdDesc {
+    MlpDesc mlp;
+    GridDesc grid[NT_MAX_GRIDS];
+    CodecGrid cgrid[NT_MAX_GRIDS];
+    TexDesc tex[NT_MAX_TEXTURES];
+    int8_t out_tex[NT_MAX_OUTPUTS];
+    int8_t out_ch[NT_MAX_OUTPUTS];
+    int G, C, ntex;
+    int count; // samples (pixels)
+    int image_w, image_h;
+    const uint16_t *inputs; // kFwdMlp
+    const float *uvz;       // kFwdBilinear / kFwdCatmullRom
+    uint16_t *features;     // optional fp16 features
+    uint16_t *out16;        // fp16 outputs
+    float *out32;           // kFwdInference
+    float *sse;             // kFwdInference
+    int out_stride;         // outputs per sample
+    uint32_t seed;
+    float jitter, mip_min, mip_max;
+};
+
+struct AdamDesc {
+    float beta1, beta2, lr, eps, bc1, bc2;
+};
+
+// Lazy Adam over the network (train.cu:681-726).
+struct NetAdamDesc {
+    AdamDesc a;
+    int num_layers;
+    int rows[NT_MAX_LAYERS], cols[NT_MAX_LAYERS], pin[NT_MAX_LAYERS], nbias[NT_MAX_LAYERS];
+    int wstart[NT_MAX_LAYERS + 1]; // prefix over layers of rows*cols + nbias
+    uint16_t *w[NT_MAX_LAYERS];
+    float *g[NT_MAX_LAYERS], *m1[NT_MAX_LAYERS], *m2[NT_MAX_LAYERS];
+    uint16_t *b[NT_MAX_LAYERS];
+    float *bg[NT_MAX_LAYERS], *bm1[NT_MAX_LAYERS], *bm2[NT_MAX_LAYERS];
+};
+
+// Lazy Adam over flat fp32 segments (latent texels or BC6 block records).
+struct LatentAdamDesc {
+    AdamDesc a;
+    int nseg;
+    int64_t start[NT_MAX_GRIDS + 1]; // prefix of work items
+    float *w[NT_MAX_GRIDS], *g[NT_MAX_GRIDS], *m1[NT_MAX_GRIDS], *m2[NT_MAX_GRIDS];
+    int64_t n[NT_MAX_GRIDS]; // floats (unconstrained) or blocks (block records)
+    int rec;                 // block record floats (4C+16); 0 = unconstrained
+};
+
+// ---- launchers (defined next to their kernels) -------------------------------------
+enum ShapeId {
+    kShapeRef = 0,   // 12(16) -> 32 -> 32 -> 16, C = 3 (the reference network)
+    kShapeFpt = 1,   // 12(16) -> 16 -> 16 (forward_pass_test)
+    kShapeC1 = 2,    // 8(16) -> 64 -> 64 -> 16, C = 8
+    kShapeC2 = 3,    // 32 -> 64 -> 64 -> 16, C = 16
+    kShapeC4 = 4,    // 64 -> 64 -> 64 -> 64 -> 16, C = 16
+    kShapeCount = 5
+};
+
+hipError_t launch_train(int shape, int type, const TrainDesc &d, int num_wg, size_t lds,
+                        hipStream_t s);
+size_t train_lds_static(int shape);
+int train_grad_total(int shape);
+hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s);
+hipError_t launch_forward(int shape, int mode, const FwdDesc &d, hipStream_t s);
+hipError_t launch_net_adam(const NetAdamDesc &d, hipStream_t s);
+hipError_t launch_latent_adam(const LatentAdamDesc &d, hipStream_t s);
+hipError_t launch_codec_encode(const float *values, int w, int h, int C, uint8_t *blocks,
+                               hipStream_t s);
+hipError_t launch_codec_decode(const uint8_t *blocks, int w, int h, int C, float *values,
+                               hipStream_t s);
+
+} // namespace ntk

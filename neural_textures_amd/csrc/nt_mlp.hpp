@@ -1,0 +1,196 @@
+// nt_mlp.hpp — the tiny fp16 MLP on gfx950 MFMA (v_mfma_f32_32x32x16_f16).
+//
+// Replaces the tcnn warp-MMA MLP of the reference (mlp.h:18-362). Formulation: the wave
+// computes Y^T = W^T X^T, so weights are the A operand (32 output rows per tile, staged in
+// LDS as ready-to-load fragments) and activations the B operand (one sample per lane
+// column, 32 samples per wave tile). The D accumulator layout of one layer is reused, in
+// registers, as the B operand of the next layer by permuting the K index of the next
+// layer's weight fragments — activations never leave VGPRs between layers.
+//
+// Feature index carried by element e (0..7) of k-step fragment q in lane group g = lane/32:
+//   "natural" layout (network input as gathered): f = 16q + 8g + e
+//   "chained" layout (any layer output / dX):     f = 16q + 8(e>>2) + 4g + (e&3)
+// Chained fragment q is elements [8(q&1), 8(q&1)+8) of D tile q>>1.
+#pragma once
+
+#include "nt_device.hpp"
+
+namespace ntk {
+
+constexpr int kWave = 64;
+
+// Padded widths: K0 network input, H hidden, NH hidden layers, output padded to 16.
+template <int K0_, int H_, int NH_>
+struct Shape {
+    static constexpr int K0 = K0_, H = H_, NH = NH_, L = NH_ + 1, OUT = 16;
+    static_assert(K0 % 16 == 0 && K0 <= 64 && H % 16 == 0 && H <= 64 && NH >= 1 && NH <= 5,
+                  "unsupported MLP shape");
+    __host__ __device__ static constexpr int kin(int l) { return l == 0 ? K0 : H; }
+    __host__ __device__ static constexpr int kout(int l) { return l == L - 1 ? OUT : H; }
+    __host__ __device__ static constexpr int t32(int w) { return (w + 31) / 32; }
+    __host__ __device__ static constexpr int fwd_frags(int l) { return t32(kout(l)) * (kin(l) / 16); }
+    __host__ __device__ static constexpr int bwd_frags(int l) { return t32(kin(l)) * (kout(l) / 16); }
+    __host__ __device__ static constexpr int fwd_off(int l)
+    {
+        int o = 0;
+        for (int j = 0; j < l; ++j)
+            o += fwd_frags(j);
+        return o;
+    }
+    __host__ __device__ static constexpr int fwd_total() { return fwd_off(L); }
+    __host__ __device__ static constexpr int bwd_off(int l)
+    {
+        int o = fwd_total();
+        for (int j = 0; j < l; ++j)
+            o += bwd_frags(j);
+        return o;
+    }
+    __host__ __device__ static constexpr int all_frags() { return bwd_off(L); }
+    // fp32 bias rows per layer, padded to whole 32-row tiles.
+    __host__ __device__ static constexpr int bias_off(int l)
+    {
+        int o = 0;
+        for (int j = 0; j < l; ++j)
+            o += 32 * t32(kout(j));
+        return o;
+    }
+    __host__ __device__ static constexpr int bias_total() { return bias_off(L); }
+    // Gradient partial layout: per layer kout*kin weights then kout biases.
+    __host__ __device__ static constexpr int grad_off(int l)
+    {
+        int o = 0;
+        for (int j = 0; j < l; ++j)
+            o += kout(j) * kin(j) + kout(j);
+        return o;
+    }
+    __host__ __device__ static constexpr int grad_total() { return grad_off(L); }
+    // dW tiles (32x32), enumerated from the last layer down.
+    __host__ __device__ static constexpr int dw_tiles(int l) { return t32(kout(l)) * t32(kin(l)); }
+    __host__ __device__ static constexpr int dw_start(int l)
+    {
+        int o = 0;
+        for (int j = L - 1; j > l; --j)
+            o += dw_tiles(j);
+        return o;
+    }
+    __host__ __device__ static constexpr int dw_total() { return dw_start(-1); }
+};
+
+__device__ __forceinline__ int chained_feature(int q, int g, int e)
+{
+    return 16 * q + 8 * (e >> 2) + 4 * g + (e & 3);
+}
+__device__ __forceinline__ int natural_feature(int q, int g, int e) { return 16 * q + 8 * g + e; }
+
+// Network pointers and unpadded sizes, as kernels see them.
+struct MlpDesc {
+    const uint16_t *W[6];
+    const uint16_t *B[6];
+    int sizes[7];
+    int num_layers;
+};
+
+// Stage forward and backward weight fragments and fp32 biases in LDS. All threads of the
+// block take part; the caller synchronises afterwards.
+template <class S, bool FWD_ONLY = false>
+__device__ void stage_weights(const MlpDesc &m, h8 *frags, float *bias, int tid, int nthreads)
+{
+    constexpr int nfrags = FWD_ONLY ? S::fwd_total() : S::all_frags();
+    // Forward fragment (a, q) of layer l, lane (c, g), element e: W_l[k][n] with
+    // n = 32a + c and k the layer's input feature for (q, g, e).
+    for (int idx = tid; idx < nfrags * kWave; idx += nthreads) {
+        const int f = idx / kWave, lane = idx % kWave, c = lane & 31, g = lane >> 5;
+        h8 v;
+        int l = 0;
+        bool fwd = f < S::fwd_total();
+        if (fwd) {
+            while (l + 1 < S::L && f >= S::fwd_off(l + 1))
+                ++l;
+        } else {
+            while (l + 1 < S::L && f >= S::bwd_off(l + 1))
+                ++l;
+        }
+        const int kin = S::kin(l), kout = S::kout(l);
+        const uint16_t *W = m.W[l];
+        if (fwd) {
+            const int local = f - S::fwd_off(l), qn = kin / 16;
+            const int a = local / qn, q = local % qn;
+            const int n = 32 * a + c;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int k = l == 0 ? natural_feature(q, g, e) : chained_feature(q, g, e);
+                v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+            }
+        } else {
+            // Backward (dX) fragment (m, q) of layer l: A[k][kk] = W_l[k][n], k = 32m + c,
+            // n = chained output feature of (q, g, e).
+            const int local = f - S::bwd_off(l), qn = kout / 16;
+            const int mt = local / qn, q = local % qn;
+            const int k = 32 * mt + c;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int n = chained_feature(q, g, e);
+                v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+            }
+        }
+        frags[idx] = v;
+    }
+    for (int idx = tid; idx < S::bias_total(); idx += nthreads) {
+        int l = 0;
+        while (l + 1 < S::L && idx >= S::bias_off(l + 1))
+            ++l;
+        const int n = idx - S::bias_off(l);
+        bias[idx] = n < m.sizes[l + 1] ? h2f(m.B[l][n]) : 0.f;
+    }
+}
+
+// One forward layer for one 32-sample tile: acc[a] = bias + W^T x.
+template <int KQ, int NA>
+__device__ __forceinline__ void layer_forward(const h8 *frags, const float *bias, const h8 (&x)[KQ],
+                                              f16v (&acc)[NA], int lane)
+{
+    const int g = lane >> 5;
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            acc[a][e] = bias[32 * a + 8 * (e >> 2) + 4 * g + (e & 3)];
+#pragma unroll
+        for (int q = 0; q < KQ; ++q)
+            acc[a] = mfma32(frags[(a * KQ + q) * kWave + lane], x[q], acc[a]);
+    }
+}
+
+// D tiles -> chained fp16 fragments, with optional ReLU (mlp.h:35-38).
+template <int NQ, int NA, bool RELU>
+__device__ __forceinline__ void to_fragments(const f16v (&acc)[NA], h8 (&y)[NQ])
+{
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = acc[q >> 1][8 * (q & 1) + e];
+            if (RELU)
+                v = v > 0.f ? v : 0.f;
+            y[q][e] = (_Float16)v;
+        }
+    }
+}
+
+// dX for one layer: acc[m] = W dY over the layer's output features (chained dY frags).
+template <int NQ, int MA>
+__device__ __forceinline__ void layer_backward_dx(const h8 *frags, const h8 (&dy)[NQ],
+                                                  f16v (&acc)[MA], int lane)
+{
+#pragma unroll
+    for (int m = 0; m < MA; ++m) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            acc[m][e] = 0.f;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+            acc[m] = mfma32(frags[(m * NQ + q) * kWave + lane], dy[q], acc[m]);
+    }
+}
+
+} // namespace ntk

@@ -1,0 +1,771 @@
+// nt_train.hip — the fused training pass on gfx950 (replaces TrainLoopPass,
+// train.cu:818-915, with mlp.h:101-362 and util/atomic.h).
+//
+// One workgroup (4 waves) owns a 64 x 8 block of training-region positions and walks it
+// in four 16 x 8 chunks of 128 samples. Per chunk each wave takes 32 samples (one MFMA
+// tile): jittered position, latent gather into fp16 B fragments, Catmull-Rom targets for
+// the lane's output rows, MLP forward (activations kept in VGPRs), fp16 loss gradient and
+// the dX chain on MFMA. Layer by layer, the waves write their layer inputs and output
+// gradients transposed into LDS, and after a barrier compute dW = X^T dY for the whole
+// 128-sample chunk on MFMA, each wave owning a fixed subset of 32x32 dW tiles whose fp32
+// accumulators stay in registers across chunks. Bias gradients are row sums of the same
+// LDS tiles. Latent gradients are accumulated with LDS atomics into a footprint box that
+// covers every texel the block can touch, then flushed once with global float atomics.
+// The MLP gradient of the workgroup goes to a per-workgroup partial that a deterministic
+// two-stage reduction adds to the network gradients (no weight-gradient atomics).
+#include "nt_internal.hpp"
+
+namespace ntk {
+
+template <class S>
+struct TrainLayout {
+    static constexpr int frag_bytes = S::all_frags() * kWave * 16;
+    static constexpr int bias_bytes = ((S::bias_total() * 4 + 15) / 16) * 16;
+    static constexpr int max_in = S::K0 > S::H ? S::K0 : S::H;
+    static constexpr int max_out = S::H > S::OUT ? S::H : S::OUT;
+    static constexpr int xt_rows = 32 * S::t32(max_in);
+    static constexpr int dyt_rows = 32 * S::t32(max_out);
+    static constexpr int xt_off = frag_bytes + bias_bytes;
+    static constexpr int dyt_off = xt_off + xt_rows * kRowStride * 2;
+    static constexpr int fp_off = dyt_off + dyt_rows * kRowStride * 2;
+    static constexpr int slots = (S::dw_total() + 3) / 4;
+};
+
+// Per-sample bilinear footprints at mip 0 for every grid (train.cu:284-303 with z = 0).
+struct SampleFootprints {
+    int x0[NT_MAX_GRIDS], y0[NT_MAX_GRIDS];
+    float w[NT_MAX_GRIDS][4];
+};
+
+__device__ __forceinline__ void sample_footprints(const TrainDesc &d, float u, float v,
+                                                  SampleFootprints &f)
+{
+#pragma unroll
+    for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
+        if (gi < d.G) {
+            const Footprint t = bilinear_footprint(u, v, d.grid[gi].w, d.grid[gi].h, 1.f - 0.f);
+            f.x0[gi] = t.x0;
+            f.y0[gi] = t.y0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                f.w[gi][c] = t.w[c];
+        } else {
+            f.x0[gi] = f.y0[gi] = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                f.w[gi][c] = 0.f;
+        }
+    }
+}
+
+// Select grid gi's footprint without dynamic register indexing.
+__device__ __forceinline__ void pick_footprint(const SampleFootprints &f, int gi, int &x0,
+                                               int &y0, float (&w)[4])
+{
+    x0 = f.x0[0];
+    y0 = f.y0[0];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        w[c] = f.w[0][c];
+#pragma unroll
+    for (int k = 1; k < NT_MAX_GRIDS; ++k) {
+        if (gi == k) {
+            x0 = f.x0[k];
+            y0 = f.y0[k];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                w[c] = f.w[k][c];
+        }
+    }
+}
+
+__device__ __forceinline__ const GridDesc &grid_ref(const TrainDesc &d, int gi)
+{
+    return d.grid[gi];
+}
+
+// Unconstrained latent gather into natural-layout B fragments: lane group g of a sample
+// holds features 16q + 8g + e. Corner contributions are rounded to fp16 and summed in
+// fp16, corner by corner (train.cu:293-310).
+template <int C, int KQ>
+__device__ __forceinline__ void gather_unconstrained(const TrainDesc &d, const SampleFootprints &f,
+                                                     int g, h8 (&x)[KQ])
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+        h8 acc;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            acc[e] = (_Float16)0.f;
+        if constexpr (C == 16 || C == 8) {
+            const int gi = C == 16 ? q : 2 * q + g;
+            const int cb = C == 16 ? 8 * g : 0;
+            if (gi < d.G) {
+                int x0, y0;
+                float w[4];
+                pick_footprint(f, gi, x0, y0, w);
+                const float *vals = C == 16 ? d.grid[q].values
+                                            : (g ? d.grid[(2 * q + 1) & 3].values : d.grid[2 * q].values);
+                const int gw = C == 16 ? d.grid[q].w : (g ? d.grid[(2 * q + 1) & 3].w : d.grid[2 * q].w);
+                const int gh = C == 16 ? d.grid[q].h : (g ? d.grid[(2 * q + 1) & 3].h : d.grid[2 * q].h);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int tx = wrap_coord(x0 + (c & 1), gw);
+                    const int ty = wrap_coord(y0 + (c >> 1), gh);
+                    const float4 *p = (const float4 *)(vals + ((int64_t)ty * gw + tx) * C + cb);
+                    const float4 a = p[0], b = p[1];
+                    const float wc = w[c];
+                    acc[0] = acc[0] + (_Float16)(wc * a.x);
+                    acc[1] = acc[1] + (_Float16)(wc * a.y);
+                    acc[2] = acc[2] + (_Float16)(wc * a.z);
+                    acc[3] = acc[3] + (_Float16)(wc * a.w);
+                    acc[4] = acc[4] + (_Float16)(wc * b.x);
+                    acc[5] = acc[5] + (_Float16)(wc * b.y);
+                    acc[6] = acc[6] + (_Float16)(wc * b.z);
+                    acc[7] = acc[7] + (_Float16)(wc * b.w);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int feat = 16 * q + 8 * g + e;
+                if (feat < d.G * C) {
+                    const int gi = feat / C, ch = feat % C;
+                    int x0, y0;
+                    float w[4];
+                    pick_footprint(f, gi, x0, y0, w);
+                    const GridDesc &gr = grid_ref(d, gi);
+                    _Float16 a = (_Float16)0.f;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int tx = wrap_coord(x0 + (c & 1), gr.w);
+                        const int ty = wrap_coord(y0 + (c >> 1), gr.h);
+                        a = a + (_Float16)(w[c] * gr.values[((int64_t)ty * gr.w + tx) * C + ch]);
+                    }
+                    acc[e] = a;
+                }
+            }
+        }
+        x[q] = acc;
+    }
+}
+
+// BC6 block record of texel (x, y) at mip 0 (train.cu:204-212, 240-261).
+struct Bc6Texel {
+    int64_t block;
+    int pix, part, bits;
+};
+__device__ __forceinline__ Bc6Texel bc6_locate(const GridDesc &gr, int C, int x, int y)
+{
+    Bc6Texel t;
+    const int nbu = (gr.w >> 2) > 0 ? (gr.w >> 2) : 1;
+    t.block = gr.block_off[0] + (int64_t)(y >> 2) * nbu + (x >> 2);
+    t.pix = ((y & 3) << 2) + (x & 3);
+    const float *rec = gr.block_params + t.block * (4 * C + 18);
+    const int partition = __float_as_int(rec[4 * C + 16]);
+    const int mode = __float_as_int(rec[4 * C + 17]);
+    t.part = (bc6_partition_mask(partition) >> t.pix) & 1;
+    t.bits = bc6_mode_bits(mode);
+    return t;
+}
+
+// BC6 latent gather: half += float (the fp32 sum rounded to fp16, train.cu:341-369).
+template <int C, int KQ>
+__device__ __forceinline__ void gather_bc6(const TrainDesc &d, const SampleFootprints &f, int g,
+                                           h8 (&x)[KQ])
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int feat = 16 * q + 8 * g + e;
+            _Float16 a = (_Float16)0.f;
+            if (feat < d.G * C) {
+                const int gi = feat / C, ch = feat % C;
+                int x0, y0;
+                float w[4];
+                pick_footprint(f, gi, x0, y0, w);
+                const GridDesc &gr = grid_ref(d, gi);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int tx = wrap_coord(x0 + (c & 1), gr.w);
+                    const int ty = wrap_coord(y0 + (c >> 1), gr.h);
+                    const Bc6Texel t = bc6_locate(gr, C, tx, ty);
+                    const float *rec = gr.block_params + t.block * (4 * C + 18);
+                    const float v = bc6_decompress(rec[2 * t.part * C + ch],
+                                                   rec[(2 * t.part + 1) * C + ch], t.bits,
+                                                   rec[4 * C + t.pix]);
+                    a = (_Float16)((float)a + w[c] * v);
+                }
+            }
+            x[q][e] = a;
+        }
+    }
+}
+
+// Catmull-Rom targets for the lane's eight output rows o = chained_feature(0, g, e)
+// (train.cu:105-157; 16 taps, exact weights).
+__device__ __forceinline__ void lane_targets(const TrainDesc &d, float u, float v, int g,
+                                             float (&t)[8], float (&wt)[8])
+{
+    int oti[8], och[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int o = chained_feature(0, g, e);
+        oti[e] = d.out_tex[o];
+        och[e] = d.out_ch[o];
+        wt[e] = d.out_w[o];
+        t[e] = 0.f;
+    }
+    for (int ti = 0; ti < d.ntex; ++ti) {
+        bool need = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            need |= oti[e] == ti;
+        if (!need)
+            continue;
+        const TexDesc tx = d.tex[ti];
+        float wx[4], wy[4];
+        const int x0 = cr_axis(u, tx.w, wx);
+        const int y0 = cr_axis(v, tx.h, wy);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 4; ++j) {
+            const int y = wrap_coord(y0 + j, tx.h);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int x = wrap_coord(x0 + i, tx.w);
+                const float wxy = wx[i] * wy[j];
+                const int64_t base = ((int64_t)y * tx.w + x) * tx.pitch;
+                if (tx.pitch == 4) {
+                    const float4 p = *(const float4 *)(tx.texels + base);
+                    acc[0] = fmaf(p.x, wxy, acc[0]);
+                    if (tx.nch > 1)
+                        acc[1] = fmaf(p.y, wxy, acc[1]);
+                    if (tx.nch > 2)
+                        acc[2] = fmaf(p.z, wxy, acc[2]);
+                    if (tx.nch > 3)
+                        acc[3] = fmaf(p.w, wxy, acc[3]);
+                } else {
+                    acc[0] = fmaf(tx.texels[base], wxy, acc[0]);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if (oti[e] == ti) {
+                const int c = och[e];
+                t[e] = c == 0 ? acc[0] : c == 1 ? acc[1] : c == 2 ? acc[2] : acc[3];
+            }
+        }
+    }
+}
+
+// Write fragments transposed into an LDS tile [feature][sample] (fp16).
+template <int NQ, bool CHAINED>
+__device__ __forceinline__ void store_transposed(_Float16 *buf, const h8 (&v)[NQ], int col, int g)
+{
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int row = CHAINED ? chained_feature(q, g, e) : natural_feature(q, g, e);
+            buf[row * kRowStride + col] = v[q][e];
+        }
+}
+
+// dW += X^T dY over one 128-sample chunk for the dW tiles this wave owns, and the
+// bias-gradient row sums (mlp.h:101-220).
+template <class S, int l>
+__device__ __forceinline__ void dw_phase(const _Float16 *xt, const _Float16 *dyt,
+                                         f16v (&acc)[TrainLayout<S>::slots], float &db,
+                                         int wave, int lane, int tid)
+{
+    constexpr int kin = S::kin(l), kout = S::kout(l);
+    constexpr int KB = S::t32(kin), NA = S::t32(kout);
+    constexpr int start = S::dw_start(l), ntiles = NA * KB;
+    const int c = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < TrainLayout<S>::slots; ++j) {
+        const int t = 4 * j + wave - start;
+        if (t >= 0 && t < ntiles) {
+            const int a = t / KB, b = t % KB;
+            const bool arow = 32 * a + c < kout, brow = 32 * b + c < kin;
+            const _Float16 *pa = dyt + (32 * a + c) * kRowStride + 8 * g;
+            const _Float16 *pb = xt + (32 * b + c) * kRowStride + 8 * g;
+#pragma unroll
+            for (int q = 0; q < kChunk / 16; ++q) {
+                h8 A = *(const h8 *)(pa + 16 * q);
+                h8 B = *(const h8 *)(pb + 16 * q);
+                if (!arow)
+                    A = (h8)(_Float16)0.f;
+                if (!brow)
+                    B = (h8)(_Float16)0.f;
+                acc[j] = mfma32(A, B, acc[j]);
+            }
+        }
+    }
+    if (tid < 4 * kout) {
+        const int n = tid >> 2, part = tid & 3;
+        const h8 *row = (const h8 *)(dyt + n * kRowStride + 32 * part);
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const h8 r = row[k];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                s += (float)r[e];
+        }
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        if (part == 0)
+            db += s;
+    }
+}
+
+// Latent gradient scatter of one sample (train.cu:460-509): LDS footprint box when the
+// texel is inside it, global float atomics otherwise.
+template <int C, int KQ>
+__device__ __forceinline__ void scatter_unconstrained(const TrainDesc &d, const SampleFootprints &f,
+                                                      const int (&flo_x)[NT_MAX_GRIDS],
+                                                      const int (&flo_y)[NT_MAX_GRIDS], float *fp,
+                                                      const h8 (&dx)[KQ], int g)
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int feat = chained_feature(q, g, e);
+            const float grad = (float)dx[q][e];
+            if (feat >= d.G * C || grad == 0.f)
+                continue;
+            const int gi = feat / C, ch = feat % C;
+            int x0, y0;
+            float w[4];
+            pick_footprint(f, gi, x0, y0, w);
+            const GridDesc &gr = grid_ref(d, gi);
+            int lox = flo_x[0], loy = flo_y[0];
+#pragma unroll
+            for (int k = 1; k < NT_MAX_GRIDS; ++k)
+                if (gi == k) {
+                    lox = flo_x[k];
+                    loy = flo_y[k];
+                }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float val = w[c] * grad;
+                const int tx = x0 + (c & 1), ty = y0 + (c >> 1);
+                const int lx = tx - lox, ly = ty - loy;
+                if (d.fp_floats > 0 && lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h) {
+                    lds_add(fp + gr.fp_off + (ly * gr.fp_w + lx) * C + ch, val);
+                } else {
+                    const int wx = wrap_coord(tx, gr.w), wy = wrap_coord(ty, gr.h);
+                    global_add(gr.grads + ((int64_t)wy * gr.w + wx) * C + ch, val);
+                }
+            }
+        }
+}
+
+// BC6 backward of one sample (train.cu:373-458), straight to global atomics.
+template <int C, int KQ>
+__device__ __forceinline__ void scatter_bc6(const TrainDesc &d, const SampleFootprints &f,
+                                            const h8 (&dx)[KQ], int g)
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int feat = chained_feature(q, g, e);
+            if (feat >= d.G * C)
+                continue;
+            const float grad = (float)dx[q][e];
+            const int gi = feat / C, ch = feat % C;
+            int x0, y0;
+            float w[4];
+            pick_footprint(f, gi, x0, y0, w);
+            const GridDesc &gr = grid_ref(d, gi);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int tx = wrap_coord(x0 + (c & 1), gr.w);
+                const int ty = wrap_coord(y0 + (c >> 1), gr.h);
+                const Bc6Texel t = bc6_locate(gr, C, tx, ty);
+                const float *rec = gr.block_params + t.block * (4 * C + 18);
+                float *grec = gr.block_grads + t.block * (4 * C + 16);
+                const int base = 2 * t.part;
+                const float xi = rec[4 * C + t.pix];
+                const float q0 = bc6_unquantize(rec[base * C + ch], t.bits);
+                const float q1 = bc6_unquantize(rec[(base + 1) * C + ch], t.bits);
+                const int hy = bc6_hy(bc6_y(q0, q1, xi));
+                const float dl_dy = ldexpf(w[c] * grad, hy - 24);
+                const float dy_dx = ldexpf(q1 - q0, 3);
+                const float alpha = ldexpf(xi, 3);
+                const float deibar = ldexpf(31.f / 64.f, 16 - t.bits);
+                global_add(grec + base * C + ch, ((1.f - alpha) * deibar) * dl_dy);
+                global_add(grec + (base + 1) * C + ch, (alpha * deibar) * dl_dy);
+                global_add(grec + 4 * C + t.pix, dl_dy * dy_dx);
+            }
+        }
+}
+
+// Backward through hidden layer l (its input is hidden activation l-1), then l-1 ... 1.
+template <class S, int l>
+__device__ __forceinline__ void backward_hidden(_Float16 *xt, _Float16 *dyt, const h8 *frags,
+                                                const h8 (&xh)[S::NH][S::H / 16],
+                                                h8 (&dyh)[S::H / 16],
+                                                f16v (&dwacc)[TrainLayout<S>::slots],
+                                                float (&dbacc)[S::L], int col, int wave, int lane,
+                                                int tid)
+{
+    if constexpr (l >= 1) {
+        constexpr int HQ = S::H / 16, HA = S::t32(S::H);
+        const int g = lane >> 5;
+        store_transposed<HQ, true>(dyt, dyh, col, g);
+        store_transposed<HQ, true>(xt, xh[l - 1], col, g);
+        f16v acc[HA];
+        layer_backward_dx<HQ, HA>(frags + S::bwd_off(l) * kWave, dyh, acc, lane);
+#pragma unroll
+        for (int q = 0; q < HQ; ++q)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                dyh[q][e] = xh[l - 1][q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e]
+                                                           : (_Float16)0.f;
+        __syncthreads();
+        dw_phase<S, l>(xt, dyt, dwacc, dbacc[l], wave, lane, tid);
+        __syncthreads();
+        backward_hidden<S, l - 1>(xt, dyt, frags, xh, dyh, dwacc, dbacc, col, wave, lane, tid);
+    }
+}
+
+template <class S, int C, int TYPE>
+__global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
+{
+    using LY = TrainLayout<S>;
+    constexpr int L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
+    extern __shared__ __align__(16) unsigned char smem[];
+    h8 *frags = (h8 *)smem;
+    float *bias = (float *)(smem + LY::frag_bytes);
+    _Float16 *xt = (_Float16 *)(smem + LY::xt_off);
+    _Float16 *dyt = (_Float16 *)(smem + LY::dyt_off);
+    float *fp = (float *)(smem + LY::fp_off);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
+    stage_weights<S>(d.mlp, frags, bias, tid, kTrainThreads);
+    for (int i = tid; i < d.fp_floats; i += kTrainThreads)
+        fp[i] = 0.f;
+
+    const int tile_x = blockIdx.x % d.tiles_x, tile_y = blockIdx.x / d.tiles_x;
+    const int tx0 = tile_x * kChunkW * d.chunks_per_wg, ty0 = tile_y * kChunkH;
+    // Footprint box origin per grid: lowest texel any sample of this block can touch.
+    int flo_x[NT_MAX_GRIDS], flo_y[NT_MAX_GRIDS];
+#pragma unroll
+    for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
+        const GridDesc &gr = d.grid[gi];
+        flo_x[gi] = (int)floorf((float)(d.off_x + tx0) * (float)gr.w / (float)d.image_w - 0.5f) - 1;
+        flo_y[gi] = (int)floorf((float)(d.off_y + ty0) * (float)gr.h / (float)d.image_h - 0.5f) - 1;
+    }
+    __syncthreads();
+
+    f16v dwacc[LY::slots];
+#pragma unroll
+    for (int j = 0; j < LY::slots; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            dwacc[j][e] = 0.f;
+    float dbacc[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+        dbacc[l] = 0.f;
+
+    const int col = 32 * wave + c; // column of this lane's sample in the LDS transposes
+    for (int chunk = 0; chunk < d.chunks_per_wg; ++chunk) {
+        // ---- sample position (train.cu:827-844)
+        const int sx = tx0 + chunk * kChunkW + (c & 15);
+        const int sy = ty0 + 2 * wave + (c >> 4);
+        const uint32_t sidx = (uint32_t)sy * (uint32_t)d.region_w + (uint32_t)sx;
+        const bool valid = sx < d.region_w && sidx < (uint32_t)d.num_samples;
+        uint32_t st = mix_seed(sidx, d.step);
+        const float jx = uniform01(st) - 0.5f;
+        const float jy = uniform01(st) - 0.5f;
+        const float px = clampf((float)(uint32_t)(d.off_x + sx) + 0.5f + jx, 0.5f,
+                                (float)d.image_w - 0.5f);
+        const float py = clampf((float)(uint32_t)(d.off_y + sy) + 0.5f + jy, 0.5f,
+                                (float)d.image_h - 0.5f);
+        const float u = px / (float)d.image_w;
+        const float v = py / (float)d.image_h;
+
+        SampleFootprints fps;
+        sample_footprints(d, u, v, fps);
+        h8 x0[KQ0];
+        if (valid) {
+            if constexpr (TYPE == NT_UNCONSTRAINED)
+                gather_unconstrained<C, KQ0>(d, fps, g, x0);
+            else
+                gather_bc6<C, KQ0>(d, fps, g, x0);
+        } else {
+#pragma unroll
+            for (int q = 0; q < KQ0; ++q)
+                x0[q] = (h8)(_Float16)0.f;
+        }
+        float tgt[8], tw[8];
+        lane_targets(d, u, v, g, tgt, tw);
+
+        // ---- forward (mlp.h:65-99)
+        h8 xh[NH][HQ];
+        {
+            f16v acc[HA];
+            layer_forward<KQ0, HA>(frags + S::fwd_off(0) * kWave, bias + S::bias_off(0), x0, acc, lane);
+            to_fragments<HQ, HA, true>(acc, xh[0]);
+#pragma unroll
+            for (int l = 1; l < NH; ++l) {
+                layer_forward<HQ, HA>(frags + S::fwd_off(l) * kWave, bias + S::bias_off(l), xh[l - 1],
+                                      acc, lane);
+                to_fragments<HQ, HA, true>(acc, xh[l]);
+            }
+        }
+        // ---- loss gradient (train.cu:876-888): dL/dy = fp16(2 w (y - t) / N)
+        h8 dyo[1];
+        {
+            f16v out[1];
+            layer_forward<HQ, 1>(frags + S::fwd_off(L - 1) * kWave, bias + S::bias_off(L - 1),
+                                 xh[NH - 1], out, lane);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float y = (float)(_Float16)out[0][e];
+                const float err = y - tgt[e];
+                const float gr = 2.f * tw[e] * err / (float)d.num_samples;
+                dyo[0][e] = valid ? (_Float16)gr : (_Float16)0.f;
+            }
+        }
+
+        // ---- backward, last layer (mlp.h:302-362)
+        h8 dyh[HQ];
+        store_transposed<1, true>(dyt, dyo, col, g);
+        store_transposed<HQ, true>(xt, xh[NH - 1], col, g);
+        {
+            f16v acc[HA];
+            layer_backward_dx<1, HA>(frags + S::bwd_off(L - 1) * kWave, dyo, acc, lane);
+#pragma unroll
+            for (int q = 0; q < HQ; ++q)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    dyh[q][e] = xh[NH - 1][q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e]
+                                                                : (_Float16)0.f;
+        }
+        __syncthreads();
+        dw_phase<S, L - 1>(xt, dyt, dwacc, dbacc[L - 1], wave, lane, tid);
+        __syncthreads();
+
+        // ---- hidden layers L-2 .. 1
+        backward_hidden<S, L - 2>(xt, dyt, frags, xh, dyh, dwacc, dbacc, col, wave, lane, tid);
+
+        // ---- first layer: dW with the natural-layout inputs, dX = input gradient
+        store_transposed<HQ, true>(dyt, dyh, col, g);
+        store_transposed<KQ0, false>(xt, x0, col, g);
+        h8 dx0[KQ0];
+        if constexpr (TYPE != NT_FINALIZE) {
+            constexpr int MA = S::t32(S::K0);
+            f16v acc[MA];
+            layer_backward_dx<HQ, MA>(frags + S::bwd_off(0) * kWave, dyh, acc, lane);
+#pragma unroll
+            for (int q = 0; q < KQ0; ++q)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    dx0[q][e] = (_Float16)acc[q >> 1][8 * (q & 1) + e];
+        }
+        __syncthreads();
+        dw_phase<S, 0>(xt, dyt, dwacc, dbacc[0], wave, lane, tid);
+        __syncthreads();
+
+        // ---- latent gradient scatter
+        if constexpr (TYPE == NT_UNCONSTRAINED) {
+            if (valid)
+                scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
+        } else if constexpr (TYPE == NT_BLOCK_FEATURES) {
+            if (valid)
+                scatter_bc6<C, KQ0>(d, fps, dx0, g);
+        }
+    }
+
+    __syncthreads();
+    // ---- flush the latent footprint box
+    if constexpr (TYPE == NT_UNCONSTRAINED) {
+        for (int i = tid; i < d.fp_floats; i += kTrainThreads) {
+            const float val = fp[i];
+            if (val == 0.f)
+                continue;
+            int gi = 0;
+#pragma unroll
+            for (int k = 1; k < NT_MAX_GRIDS; ++k)
+                if (k < d.G && i >= d.grid[k].fp_off)
+                    gi = k;
+            const GridDesc &gr = d.grid[gi];
+            const int local = i - gr.fp_off;
+            const int ch = local % C, cell = local / C;
+            const int lx = cell % gr.fp_w, ly = cell / gr.fp_w;
+            const int wx = wrap_coord(flo_x[gi] + lx, gr.w), wy = wrap_coord(flo_y[gi] + ly, gr.h);
+            global_add(gr.grads + ((int64_t)wy * gr.w + wx) * C + ch, val);
+        }
+    }
+    // ---- per-workgroup MLP gradient partial
+    float *part = d.partial + (int64_t)blockIdx.x * S::grad_total();
+#pragma unroll
+    for (int j = 0; j < LY::slots; ++j) {
+        const int t = 4 * j + wave;
+        if (t < S::dw_total()) {
+            int l = 0;
+#pragma unroll
+            for (int k = 0; k < L; ++k)
+                if (t >= S::dw_start(k) && t < S::dw_start(k) + S::dw_tiles(k))
+                    l = k;
+            int kin = S::kin(0), kout = S::kout(0), start = S::dw_start(0), off = S::grad_off(0);
+#pragma unroll
+            for (int k = 1; k < L; ++k)
+                if (l == k) {
+                    kin = S::kin(k);
+                    kout = S::kout(k);
+                    start = S::dw_start(k);
+                    off = S::grad_off(k);
+                }
+            const int kb = (kin + 31) / 32;
+            const int a = (t - start) / kb, b = (t - start) % kb;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int n = 32 * a + 8 * (e >> 2) + 4 * g + (e & 3);
+                const int k = 32 * b + c;
+                if (n < kout && k < kin)
+                    part[off + n * kin + k] = dwacc[j][e];
+            }
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+        if (tid < 4 * S::kout(l) && (tid & 3) == 0)
+            part[S::grad_off(l) + S::kout(l) * S::kin(l) + (tid >> 2)] = dbacc[l];
+}
+
+// Two-stage deterministic reduction of the per-workgroup partials into the network
+// gradients (which the contract says are accumulated into, train.cu:1028-1048).
+__global__ __launch_bounds__(256) void reduce_stage1(ReduceDesc d)
+{
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= d.P)
+        return;
+    const int r0 = blockIdx.y * d.rows_per_block;
+    const int r1 = min(r0 + d.rows_per_block, d.rows);
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int r = r0;
+    for (; r + 4 <= r1; r += 4) {
+        s0 += d.partial[(int64_t)r * d.P + p];
+        s1 += d.partial[(int64_t)(r + 1) * d.P + p];
+        s2 += d.partial[(int64_t)(r + 2) * d.P + p];
+        s3 += d.partial[(int64_t)(r + 3) * d.P + p];
+    }
+    for (; r < r1; ++r)
+        s0 += d.partial[(int64_t)r * d.P + p];
+    d.tmp[(int64_t)blockIdx.y * d.P + p] = (s0 + s1) + (s2 + s3);
+}
+
+__global__ __launch_bounds__(256) void reduce_stage2(ReduceDesc d)
+{
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= d.P)
+        return;
+    float s = 0.f;
+    for (int r = 0; r < d.stage1_blocks; ++r)
+        s += d.tmp[(int64_t)r * d.P + p];
+    int l = 0;
+    for (int k = 1; k < d.num_layers; ++k)
+        if (p >= d.off[k])
+            l = k;
+    const int local = p - d.off[l];
+    const int nw = d.kin[l] * d.kout[l];
+    if (local < nw) {
+        d.wgrad[l][local] += s;
+    } else if (local - nw < d.nbias[l]) {
+        d.bgrad[l][local - nw] += s;
+    }
+}
+
+hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s)
+{
+    dim3 g1((d.P + 255) / 256, d.stage1_blocks);
+    hipLaunchKernelGGL(reduce_stage1, g1, dim3(256), 0, s, d);
+    hipLaunchKernelGGL(reduce_stage2, dim3((d.P + 255) / 256), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
+template <class S, int C, int TYPE>
+static hipError_t launch_one(const TrainDesc &d, int num_wg, size_t lds, hipStream_t s)
+{
+    auto k = train_kernel<S, C, TYPE>;
+    static size_t configured = 0;
+    if (lds > 65536 && lds > configured) {
+        hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds);
+        if (e != hipSuccess)
+            return e;
+        configured = lds;
+    }
+    hipLaunchKernelGGL(k, dim3(num_wg), dim3(kTrainThreads), lds, s, d);
+    return hipGetLastError();
+}
+
+template <class S, int C>
+static hipError_t launch_typed(int type, const TrainDesc &d, int num_wg, size_t lds, hipStream_t s)
+{
+    switch (type) {
+    case NT_UNCONSTRAINED:
+        return launch_one<S, C, NT_UNCONSTRAINED>(d, num_wg, lds, s);
+    case NT_BLOCK_FEATURES:
+        return launch_one<S, C, NT_BLOCK_FEATURES>(d, num_wg, lds, s);
+    default:
+        return launch_one<S, C, NT_FINALIZE>(d, num_wg, lds, s);
+    }
+}
+
+using ShapeRef = Shape<16, 32, 2>;
+using ShapeC2 = Shape<32, 64, 2>;
+using ShapeC4 = Shape<64, 64, 3>;
+
+hipError_t launch_train(int shape, int type, const TrainDesc &d, int num_wg, size_t lds, hipStream_t s)
+{
+    switch (shape) {
+    case kShapeRef:
+        return launch_typed<ShapeRef, 3>(type, d, num_wg, lds, s);
+    case kShapeC2:
+        return launch_typed<ShapeC2, 16>(type, d, num_wg, lds, s);
+    case kShapeC4:
+        return launch_typed<ShapeC4, 16>(type, d, num_wg, lds, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+size_t train_lds_static(int shape)
+{
+    switch (shape) {
+    case kShapeRef:
+        return TrainLayout<ShapeRef>::fp_off;
+    case kShapeC2:
+        return TrainLayout<ShapeC2>::fp_off;
+    case kShapeC4:
+        return TrainLayout<ShapeC4>::fp_off;
+    default:
+        return 0;
+    }
+}
+
+int train_grad_total(int shape)
+{
+    switch (shape) {
+    case kShapeRef:
+        return ShapeRef::grad_total();
+    case kShapeC2:
+        return ShapeC2::grad_total();
+    case kShapeC4:
+        return ShapeC4::grad_total();
+    default:
+        return 0;
+    }
+}
+
+} // namespace ntk

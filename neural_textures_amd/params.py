@@ -1,0 +1,338 @@
+"""Latent grids, networks and reference textures laid out for the C ABI.
+
+Arrays may be numpy arrays (host memory: what the CPU oracle in the tests reads) or torch
+tensors (device memory: what libnt_hip.so reads); `to_torch` / `to_numpy` copy a whole
+set between the two. The layouts are the ones include/nt/nt.h documents:
+  latents  — flat [texel][C] fp32 per grid, mips back to back (mip_chain_layout)
+  blocks   — BC6 block records of (4C+16) floats + 2 int32 (block_chain_layout)
+  weights  — fp16 bits, column-major, padded to 16: W[col * pad16(in) + row]
+  textures — flat [texel][pitch] fp32, mip chain like the latents
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import abi
+
+
+def mip_dim(size: int, mip: int) -> int:
+    return max(size >> mip, 1)
+
+
+def mip_chain_layout(width: int, height: int, num_mips: int):
+    """Texel offset of every mip and the total (nt_mip_chain_layout)."""
+    offs, off = [], 0
+    for m in range(num_mips):
+        offs.append(off)
+        off += mip_dim(width, m) * mip_dim(height, m)
+    return offs, off
+
+
+def block_chain_layout(width: int, height: int, num_mips: int):
+    """Block offset of every mip and the total (nt_block_chain_layout)."""
+    offs, off = [], 0
+    for m in range(num_mips):
+        offs.append(off)
+        off += max(mip_dim(width, m) >> 2, 1) * max(mip_dim(height, m) >> 2, 1)
+    return offs, off
+
+
+def codec_chain_layout(width: int, height: int, num_mips: int, channels: int):
+    """Byte offset of every mip of a codec-quantized grid and the total."""
+    offs, off = [], 0
+    for m in range(num_mips):
+        offs.append(off)
+        w, h = mip_dim(width, m), mip_dim(height, m)
+        off += ((w + 3) // 4) * ((h + 3) // 4) * 12 * channels
+    return offs, off
+
+
+def _is_torch(a) -> bool:
+    return a is not None and not isinstance(a, np.ndarray)
+
+
+def address(a) -> int:
+    if a is None:
+        return 0
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()
+
+
+def pointer(a, ctype=C.c_float):
+    addr = address(a)
+    return C.cast(addr, C.POINTER(ctype)) if addr else C.POINTER(ctype)()
+
+
+def _copy(a, to_torch: bool, device):
+    if a is None:
+        return None
+    if to_torch:
+        import torch
+
+        if isinstance(a, np.ndarray):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+        return a.to(device).contiguous()
+    if isinstance(a, np.ndarray):
+        return a.copy()
+    return a.detach().cpu().numpy()
+
+
+@dataclass
+class Grid:
+    """One latent grid with its mip chain (a reference `Feature`, train.h:51-67)."""
+    width: int
+    height: int
+    num_mips: int
+    channels: int
+    values: object = None
+    grads: object = None
+    moment1: object = None
+    moment2: object = None
+    block_params: object = None
+    block_grads: object = None
+    block_moment1: object = None
+    block_moment2: object = None
+
+    @property
+    def mip_offsets(self):
+        return mip_chain_layout(self.width, self.height, self.num_mips)[0]
+
+    @property
+    def texels(self) -> int:
+        return mip_chain_layout(self.width, self.height, self.num_mips)[1]
+
+    @property
+    def blocks(self) -> int:
+        return block_chain_layout(self.width, self.height, self.num_mips)[1]
+
+    def struct(self) -> abi.nt_grid:
+        g = abi.nt_grid()
+        g.width, g.height, g.num_mips = self.width, self.height, self.num_mips
+        for m, o in enumerate(self.mip_offsets):
+            g.mip_offset[m] = o
+        for m, o in enumerate(block_chain_layout(self.width, self.height, self.num_mips)[0]):
+            g.block_offset[m] = o
+        g.values, g.grads = pointer(self.values), pointer(self.grads)
+        g.moment1, g.moment2 = pointer(self.moment1), pointer(self.moment2)
+        g.block_params, g.block_grads = pointer(self.block_params), pointer(self.block_grads)
+        g.block_moment1, g.block_moment2 = pointer(self.block_moment1), pointer(self.block_moment2)
+        return g
+
+    def converted(self, to_torch: bool, device=None) -> "Grid":
+        kw = {k: _copy(getattr(self, k), to_torch, device) for k in
+              ("values", "grads", "moment1", "moment2", "block_params", "block_grads",
+               "block_moment1", "block_moment2")}
+        return Grid(self.width, self.height, self.num_mips, self.channels, **kw)
+
+    def mip(self, arr, m: int):
+        """View of mip m of a flat [texel*C] array as [h, w, C]."""
+        o = self.mip_offsets[m]
+        w, h = mip_dim(self.width, m), mip_dim(self.height, m)
+        return arr[o * self.channels:(o + w * h) * self.channels].reshape(h, w, self.channels)
+
+
+@dataclass
+class Network:
+    """The tiny MLP (mlp.h) with Adam state; sizes[0] inputs ... sizes[-1] outputs."""
+    sizes: list
+    used_outputs: int
+    weights: list = field(default_factory=list)  # uint16 fp16 bits, padded column-major
+    biases: list = field(default_factory=list)   # uint16 fp16 bits
+    weight_grads: list = field(default_factory=list)
+    weight_moment1: list = field(default_factory=list)
+    weight_moment2: list = field(default_factory=list)
+    bias_grads: list = field(default_factory=list)
+    bias_moment1: list = field(default_factory=list)
+    bias_moment2: list = field(default_factory=list)
+
+    @property
+    def num_layers(self) -> int:
+        return len(self.sizes) - 1
+
+    def padded(self, l: int):
+        return abi.pad16(self.sizes[l]), abi.pad16(self.sizes[l + 1])
+
+    def struct(self) -> abi.nt_mlp:
+        m = abi.nt_mlp()
+        m.num_layers = self.num_layers
+        for i, s in enumerate(self.sizes):
+            m.sizes[i] = s
+        m.used_outputs = self.used_outputs
+        for l in range(self.num_layers):
+            m.weights[l] = pointer(self.weights[l], C.c_uint16)
+            m.biases[l] = pointer(self.biases[l], C.c_uint16)
+            for name in ("weight_grads", "weight_moment1", "weight_moment2", "bias_grads",
+                         "bias_moment1", "bias_moment2"):
+                lst = getattr(self, name)
+                getattr(m, name)[l] = pointer(lst[l] if l < len(lst) else None)
+        return m
+
+    def converted(self, to_torch: bool, device=None) -> "Network":
+        kw = {k: [_copy(a, to_torch, device) for a in getattr(self, k)] for k in
+              ("weights", "biases", "weight_grads", "weight_moment1", "weight_moment2",
+               "bias_grads", "bias_moment1", "bias_moment2")}
+        return Network(list(self.sizes), self.used_outputs, **kw)
+
+    def weight_matrix(self, l: int) -> np.ndarray:
+        """Layer l's fp32 weights as [out_pad, in_pad] (W[col][row])."""
+        pin, pout = self.padded(l)
+        w = self.weights[l]
+        w = w if isinstance(w, np.ndarray) else w.cpu().numpy()
+        return w.view(np.float16).astype(np.float32).reshape(pout, pin)
+
+
+@dataclass
+class Texture:
+    """A reference texture (train.h:69-77) in plain memory with wrap addressing."""
+    width: int
+    height: int
+    num_channels: int
+    texels: object  # flat [texel * pitch] fp32 over the mip chain
+    num_mips: int = 1
+    pitch: int = 4
+    loss_weight: float = 1.0
+
+    def struct(self) -> abi.nt_texture:
+        t = abi.nt_texture()
+        t.texels = pointer(self.texels)
+        t.width, t.height, t.num_channels = self.width, self.height, self.num_channels
+        t.num_mips, t.pitch, t.loss_weight = self.num_mips, self.pitch, self.loss_weight
+        for m, o in enumerate(mip_chain_layout(self.width, self.height, self.num_mips)[0]):
+            t.mip_offset[m] = o
+        return t
+
+    def converted(self, to_torch: bool, device=None) -> "Texture":
+        return Texture(self.width, self.height, self.num_channels,
+                       _copy(self.texels, to_torch, device), self.num_mips, self.pitch,
+                       self.loss_weight)
+
+
+@dataclass
+class TrainState:
+    """Everything one training configuration holds (a reference KernelParams)."""
+    grids: list
+    net: Network
+    textures: list
+    image_width: int
+    image_height: int
+    num_samples: int
+    region_width: int = abi.NT_DEFAULT_REGION
+    texel_offset_x: int = 0
+    texel_offset_y: int = 0
+    step: int = 0
+    network_adam: tuple = (0.9, 0.999, 1e-3, 1e-8)
+    feature_adam: tuple = (0.9, 0.999, 5e-2, 1e-8)
+    workspace: object = None
+    inference_output: object = None
+    inference_mse_accum: object = None
+
+    @property
+    def channels(self) -> int:
+        return self.grids[0].channels
+
+    def params(self) -> abi.nt_params:
+        p = abi.nt_params()
+        p.latents.num_grids = len(self.grids)
+        p.latents.channels = self.channels
+        for i, g in enumerate(self.grids):
+            p.latents.grids[i] = g.struct()
+        p.mlp = self.net.struct()
+        p.network_adam = abi.nt_adam(*self.network_adam)
+        p.feature_adam = abi.nt_adam(*self.feature_adam)
+        for i, t in enumerate(self.textures):
+            p.textures[i] = t.struct()
+        p.num_textures = len(self.textures)
+        p.image_width, p.image_height = self.image_width, self.image_height
+        p.texel_offset_x, p.texel_offset_y = self.texel_offset_x, self.texel_offset_y
+        p.region_width, p.num_samples, p.step = self.region_width, self.num_samples, self.step
+        p.inference_output = pointer(self.inference_output)
+        p.inference_mse_accum = pointer(self.inference_mse_accum)
+        if self.workspace is not None:
+            p.workspace = C.c_void_p(address(self.workspace))
+            p.workspace_bytes = self.workspace.numel() * self.workspace.element_size() \
+                if _is_torch(self.workspace) else self.workspace.nbytes
+        return p
+
+    def converted(self, to_torch: bool, device=None) -> "TrainState":
+        return TrainState(
+            [g.converted(to_torch, device) for g in self.grids],
+            self.net.converted(to_torch, device),
+            [t.converted(to_torch, device) for t in self.textures],
+            self.image_width, self.image_height, self.num_samples, self.region_width,
+            self.texel_offset_x, self.texel_offset_y, self.step, self.network_adam,
+            self.feature_adam, None,
+            _copy(self.inference_output, to_torch, device),
+            _copy(self.inference_mse_accum, to_torch, device))
+
+    def to_torch(self, device="cuda") -> "TrainState":
+        return self.converted(True, device)
+
+    def to_numpy(self) -> "TrainState":
+        return self.converted(False)
+
+
+# ---- seeded construction (host, numpy) ----------------------------------------------
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def make_network(sizes, used_outputs=None, rng=None, scale=None, init="uniform") -> Network:
+    """fp16 weights, zero padding, zero biases (main.cpp:182-201, 735-793). init="xavier"
+    draws U[-sqrt(6/(in+out)), +] per layer; otherwise U[-scale, scale] (default 1e-2)."""
+    rng = rng if rng is not None else np.random.default_rng(1337)
+    used = sizes[-1] if used_outputs is None else used_outputs
+    net = Network(list(sizes), used)
+    for l in range(len(sizes) - 1):
+        pin, pout = abi.pad16(sizes[l]), abi.pad16(sizes[l + 1])
+        cols = used if l == len(sizes) - 2 else sizes[l + 1]
+        a = np.sqrt(6.0 / (sizes[l] + sizes[l + 1])) if init == "xavier" else (scale or 1e-2)
+        w = np.zeros((pout, pin), np.float32)
+        w[:cols, :sizes[l]] = rng.uniform(-a, a, size=(cols, sizes[l]))
+        net.weights.append(f16_bits(w.reshape(-1)))
+        net.biases.append(np.zeros(sizes[l + 1], np.uint16))
+        net.weight_grads.append(np.zeros(pin * pout, np.float32))
+        net.weight_moment1.append(np.zeros(pin * pout, np.float32))
+        net.weight_moment2.append(np.zeros(pin * pout, np.float32))
+        net.bias_grads.append(np.zeros(sizes[l + 1], np.float32))
+        net.bias_moment1.append(np.zeros(sizes[l + 1], np.float32))
+        net.bias_moment2.append(np.zeros(sizes[l + 1], np.float32))
+    return net
+
+
+def make_grid(width, height, num_mips, channels, rng=None, low=-1.0, high=1.0,
+              with_adam=True, blocks=False) -> Grid:
+    rng = rng if rng is not None else np.random.default_rng(1337)
+    g = Grid(width, height, num_mips, channels)
+    n = g.texels * channels
+    g.values = rng.uniform(low, high, size=n).astype(np.float32)
+    if with_adam:
+        g.grads = np.zeros(n, np.float32)
+        g.moment1 = np.zeros(n, np.float32)
+        g.moment2 = np.zeros(n, np.float32)
+    if blocks:
+        nb = g.blocks
+        rec = 4 * channels + 16
+        params = np.zeros((nb, rec + 2), np.float32)
+        params[:, :4 * channels] = rng.uniform(0.0, 0.05, size=(nb, 4 * channels))
+        params[:, 4 * channels:rec] = rng.uniform(0.0, 0.125, size=(nb, 16))
+        ints = params.view(np.int32)
+        ints[:, rec] = rng.integers(0, 32, size=nb)
+        ints[:, rec + 1] = rng.integers(0, 10, size=nb)
+        g.block_params = params.reshape(-1)
+        g.block_grads = np.zeros(nb * rec, np.float32)
+        g.block_moment1 = np.zeros(nb * rec, np.float32)
+        g.block_moment2 = np.zeros(nb * rec, np.float32)
+    return g
+
+
+def make_texture(width, height, num_channels, data: np.ndarray, loss_weight=1.0) -> Texture:
+    """data: [h, w, nch] fp32 (mip 0 only)."""
+    pitch = 1 if num_channels == 1 else 4
+    t = np.zeros((height, width, pitch), np.float32)
+    t[:, :, :min(num_channels, pitch)] = data[:, :, :min(num_channels, pitch)]
+    return Texture(width, height, num_channels, t.reshape(-1), 1, pitch, loss_weight)

@@ -1,0 +1,109 @@
+/*
+ * nt_oracle.h — scalar CPU restatement of mavenkim2/neural_textures' train/decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This code is the parity checker for the HIP library and the
+ * CPU baseline timed by bench.py; the product never links, loads or calls it. Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg use it.
+ *
+ * It works on host memory laid out exactly as the device buffers described in
+ * include/nt/nt.h (the same structs, holding host pointers). Every function cites the
+ * reference file:line it restates. Floating-point policy (shared with the HIP kernels so
+ * that both produce identical bits where the arithmetic is deterministic):
+ *   - compiled with -ffp-contract=off; an explicit fmaf() stands wherever nvcc's default
+ *     contraction would fuse a product into an add in the reference source;
+ *   - fp16 conversions round to nearest even and keep subnormals;
+ *   - MLP dot products accumulate in double here (the GPU accumulates in fp32 MFMA);
+ *     results are compared with a tolerance, as the reference itself is order-
+ *     nondeterministic (float atomics).
+ */
+#ifndef NT_ORACLE_H
+#define NT_ORACLE_H
+
+#include <stdint.h>
+#include "../include/nt/nt.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar helpers ---------------------------------------------------------------- */
+uint16_t ntref_f32_to_f16(float f);
+float ntref_f16_to_f32(uint16_t h);
+uint16_t ntref_f16_add(uint16_t a, uint16_t b);
+uint32_t ntref_xorshift32(uint32_t *state);
+float ntref_uniform(uint32_t *state);
+uint32_t ntref_sample_seed(uint32_t sample_index, int step);
+
+/* Sample position of sample i (train.cu:827-844): writes (u, v, 0). */
+void ntref_sample_uvz(const nt_params *p, uint32_t sample_index, float uvz[3]);
+
+/* Latent sampling: bilinear/trilinear with fp16 accumulation (train.cu:263-314). */
+void ntref_sample_latents_bilinear(const nt_latents *lat, const float uvz[3], uint16_t *out);
+/* 16-tap Catmull-Rom on mip 0 of every grid, fp32 accumulation, fp16 result. */
+void ntref_sample_latents_catmull_rom(const nt_latents *lat, const float uvz[3], uint16_t *out);
+/* Differentiable BC6 block latents (train.cu:316-371). */
+void ntref_sample_latents_bc6(const nt_latents *lat, const float uvz[3], uint16_t *out);
+
+/* Latent gradient scatter of one sample: grads += corner weight * dinput
+ * (train.cu:460-509), and its BC6 counterpart (train.cu:373-458). */
+void ntref_scatter_unconstrained(const nt_latents *lat, const float uvz[3], const uint16_t *dinput);
+void ntref_scatter_bc6(const nt_latents *lat, const float uvz[3], const uint16_t *dinput);
+
+/* Catmull-Rom weights for fractional offset f (filter/catmull_rom.h:56-59). */
+void ntref_catmull_rom_weights(float f, float w[4]);
+/* Reference-texture sample with Catmull-Rom at mip coordinate z (train.cu:78-103). */
+void ntref_sample_texture(const nt_texture *t, float u, float v, float z, float out[4]);
+/* Target packing (train.cu:105-157). Returns the number of packed channels. */
+int ntref_expected_values(const nt_params *p, const float uvz[3], float expected[16],
+                          float weights[16]);
+
+/* BC6 emulation (train.cu:159-202). */
+float ntref_bc6_unquantize(float e, int bits);
+float ntref_bc6_decompress(float e0, float e1, int bits, float x);
+extern const int ntref_bc6_partition_sets[32];
+extern const int ntref_bc6_partition_bits[10];
+
+/*
+ * MLP forward for one sample (mlp.h:18-99). in: sizes[0] fp16. acts (optional): the
+ * fp16 input of every layer, layer l at acts + l*64 (64 = max padded width), zero-padded.
+ * out: padded output (AlignUp(sizes[L],16)) fp16.
+ */
+void ntref_mlp_forward_one(const nt_mlp *mlp, const uint16_t *in, uint16_t *acts,
+                           uint16_t *out);
+/*
+ * MLP backward for one sample (mlp.h:222-362) given the saved layer inputs and the output
+ * gradient dy (padded, fp16). Adds weight/bias gradients into the double accumulators
+ * dw[l] (padIn*padOut) and db[l] (padOut); writes the fp16 input gradient (sizes[0]).
+ */
+void ntref_mlp_backward_one(const nt_mlp *mlp, const uint16_t *acts, const uint16_t *dy,
+                            double **dw, double **db, uint16_t *dinput);
+
+/* ---- whole passes (mirroring the C ABI) --------------------------------------------- */
+int ntref_train_step(const nt_params *p, int type, int num_threads);
+int ntref_optimize_network(const nt_params *p);
+int ntref_optimize_latents(const nt_params *p, int type);
+int ntref_inference(const nt_params *p);
+int ntref_mlp_forward(const nt_mlp *mlp, const uint16_t *inputs, uint16_t *outputs, int count);
+int ntref_forward(const nt_latents *lat, const nt_mlp *mlp, int filter, const float *uvz,
+                  int count, uint16_t *features, uint16_t *outputs);
+/* Per-sample loss gradients and targets of a train step, for debugging and tests:
+ * dy: [num_samples][16] fp16, target: [num_samples][16] fp32 (either may be NULL). */
+int ntref_train_intermediates(const nt_params *p, int type, uint16_t *features, uint16_t *dy,
+                              float *target);
+
+/* Block codec (no reference counterpart). */
+uint16_t ntref_codec_key(uint16_t h);
+uint16_t ntref_codec_unkey(uint16_t k);
+uint16_t ntref_codec_interp(uint16_t k0, uint16_t k1, int index);
+int ntref_codec_encode(const float *values, int width, int height, int channels,
+                       uint8_t *blocks);
+int ntref_codec_decode(const uint8_t *blocks, int width, int height, int channels,
+                       float *values);
+/* Decode a full image from codec latents (mirrors nt_decode). */
+int ntref_decode(const nt_decode_params *p, int num_threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,327 @@
+"""Parity of the HIP library (through the C ABI, on cuda:0) with the CPU oracle on the same
+seeded inputs.
+
+Bars (written per test): bit-exact for sampled fp16 features, targets-derived integer
+work, codec blocks and Adam updates (same IEEE operations in the same order);
+<= 1e-2 relative (norm) for fp16-MLP-derived outputs and gradients, whose fp32 MFMA
+accumulation order differs from the oracle's float64 sums.
+"""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+import neural_textures_amd as nt
+from neural_textures_amd import abi, params as P
+from helpers import make_state, rel_err, to_np, gpu_workspace
+from oracle_lib import load_oracle
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "forward_pass_test.json")
+MLP_TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch
+    assert torch.cuda.is_available()
+    return nt.load()
+
+
+@pytest.fixture(scope="module")
+def O():
+    return load_oracle()
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+# ---- MLP forward -----------------------------------------------------------------------
+
+def test_mlp_forward_known_answer(lib, O):
+    """tests/forward_pass_test.cu: |out - expected| <= 2e-2 (:236) on the HIP path."""
+    import torch
+    say("case: mlp_forward forward_pass_test fixture")
+    d = json.load(open(GOLDEN))
+    net = P.Network([12, 16, 16], 16)
+    net.weights = [np.array(d["w0_f16_bits"], np.uint16), np.array(d["w1_f16_bits"], np.uint16)]
+    net.biases = [np.array(d["b0_f16_bits"], np.uint16), np.array(d["b1_f16_bits"], np.uint16)]
+    inputs = np.array(d["inputs_f16_bits"], np.uint16)
+    expected = np.array(d["expected"], np.float32).reshape(32, 16)
+    gnet = net.converted(True, "cuda")
+    gin = torch.from_numpy(inputs.astype(np.int16)).cuda()
+    gout = torch.zeros(32 * 16, dtype=torch.int16, device="cuda")
+    m = gnet.struct()
+    nt.check(lib.nt_mlp_forward(C.byref(m), gin.data_ptr(), gout.data_ptr(), 32, None))
+    sync()
+    got = gout.cpu().numpy().view(np.float16).astype(np.float32).reshape(32, 16)
+    assert np.max(np.abs(got - expected)) <= d["tolerance_abs"]
+    oracle = np.zeros(32 * 16, np.uint16)
+    assert O.ntref_mlp_forward(C.byref(net.struct()), inputs.ctypes.data, oracle.ctypes.data, 32) == 0
+    assert rel_err(got, oracle.view(np.float16).astype(np.float32).reshape(32, 16)) <= 2e-3
+
+
+@pytest.mark.parametrize("sizes", [[12, 32, 32, 16], [8, 64, 64, 3], [32, 64, 64, 9],
+                                   [64, 64, 64, 64, 12], [12, 16, 16]])
+@pytest.mark.parametrize("count", [1, 33, 1000])
+def test_mlp_forward_random(lib, O, sizes, count):
+    import torch
+    say(f"case: mlp_forward sizes={sizes} count={count}")
+    rng = np.random.default_rng(len(sizes) * 100 + count)
+    net = P.make_network(sizes, rng=rng, init="xavier")
+    for l in range(net.num_layers):
+        net.biases[l] = P.f16_bits(rng.uniform(-0.1, 0.1, sizes[l + 1]))
+    x = P.f16_bits(rng.uniform(-1, 1, size=count * sizes[0]))
+    gnet = net.converted(True, "cuda")
+    gin = torch.from_numpy(x.astype(np.int16)).cuda()
+    gout = torch.zeros(count * sizes[-1], dtype=torch.int16, device="cuda")
+    nt.check(lib.nt_mlp_forward(C.byref(gnet.struct()), gin.data_ptr(), gout.data_ptr(), count, None))
+    sync()
+    got = gout.cpu().numpy().view(np.float16).astype(np.float32)
+    want = np.zeros(count * sizes[-1], np.uint16)
+    assert O.ntref_mlp_forward(C.byref(net.struct()), x.ctypes.data, want.ctypes.data, count) == 0
+    want = want.view(np.float16).astype(np.float32)
+    assert rel_err(got, want) <= MLP_TOL
+    assert np.max(np.abs(got - want)) <= 2e-2 * max(1.0, np.max(np.abs(want)))
+
+
+# ---- latent sample + forward (nt_forward) ------------------------------------------------
+
+@pytest.mark.parametrize("shape", ["ref", "c2", "c4"])
+@pytest.mark.parametrize("filt", [abi.NT_FILTER_BILINEAR, abi.NT_FILTER_CATMULL_ROM])
+def test_forward_features_bit_exact(lib, O, shape, filt):
+    import torch
+    say(f"case: forward shape={shape} filter={filt}")
+    st = make_state(shape, image=64, region=(32, 8), seed=3)
+    rng = np.random.default_rng(30)
+    n = 777
+    uvz = rng.uniform(0, 1, size=(n, 3)).astype(np.float32)
+    uvz[:, 2] = rng.uniform(0, 3.5, n) if filt == abi.NT_FILTER_BILINEAR else 0.0
+    uvz[:5, :2] = [[0, 0], [1, 1], [0.999, 0.0001], [0.5, 0.5], [1e-7, 0.9999999]]
+    F = st.net.sizes[0]
+    no = st.net.sizes[-1]
+    feats = np.zeros(n * F, np.uint16)
+    outs = np.zeros(n * no, np.uint16)
+    lat = st.params().latents
+    assert O.ntref_forward(C.byref(lat), C.byref(st.net.struct()), filt, uvz.ctypes.data, n,
+                           feats.ctypes.data, outs.ctypes.data) == 0
+    gs = st.to_torch()
+    gl = gs.params().latents
+    guvz = torch.from_numpy(uvz).cuda()
+    gf = torch.zeros(n * F, dtype=torch.int16, device="cuda")
+    go = torch.zeros(n * no, dtype=torch.int16, device="cuda")
+    nt.check(lib.nt_forward(C.byref(gl), C.byref(gs.net.struct()), filt, guvz.data_ptr(), n,
+                            gf.data_ptr(), go.data_ptr(), None))
+    sync()
+    assert np.array_equal(gf.cpu().numpy().view(np.uint16), feats)
+    got = go.cpu().numpy().view(np.float16).astype(np.float32)
+    assert rel_err(got, outs.view(np.float16).astype(np.float32)) <= MLP_TOL
+
+
+# ---- the fused train step -----------------------------------------------------------------
+
+TRAIN_CASES = [
+    # shape, image, region (w, h), offset, kernel type
+    ("ref", 128, (64, 32), (0, 0), abi.NT_UNCONSTRAINED),
+    ("ref", 128, (64, 32), (100, 110), abi.NT_UNCONSTRAINED),  # region wraps past the edge
+    ("c2", 128, (64, 32), (16, 40), abi.NT_UNCONSTRAINED),
+    ("c2", 64, (50, 21), (3, 5), abi.NT_UNCONSTRAINED),         # ragged region and tail row
+    ("c4", 128, (64, 32), (8, 8), abi.NT_UNCONSTRAINED),
+    ("ref", 64, (32, 16), (0, 0), abi.NT_BLOCK_FEATURES),
+    ("ref", 64, (32, 16), (5, 7), abi.NT_FINALIZE),
+]
+
+
+def run_train_pair(lib, O, shape, image, region, offset, ktype, seed=0, step=0):
+    st = make_state(shape, image=image, region=region, offset=offset, seed=seed, step=step,
+                    blocks=ktype != abi.NT_UNCONSTRAINED)
+    if region == (50, 21):
+        st.num_samples = 50 * 21 - 17  # partial last row
+    gs = gpu_workspace(lib, st.to_torch(), ktype)
+    assert O.ntref_train_step(C.byref(st.params()), ktype, 1) == 0
+    nt.check(lib.nt_train_step(C.byref(gs.params()), ktype, None))
+    sync()
+    return st, gs
+
+
+@pytest.mark.parametrize("case", TRAIN_CASES, ids=lambda c: f"{c[0]}-{c[1]}-{c[2][0]}x{c[2][1]}-{c[4]}")
+def test_train_step_gradients(lib, O, case):
+    shape, image, region, offset, ktype = case
+    say(f"case: train {case}")
+    st, gs = run_train_pair(lib, O, shape, image, region, offset, ktype)
+    for l in range(st.net.num_layers):
+        assert rel_err(to_np(gs.net.weight_grads[l]), st.net.weight_grads[l]) <= MLP_TOL, f"dW{l}"
+        assert rel_err(to_np(gs.net.bias_grads[l]), st.net.bias_grads[l]) <= MLP_TOL, f"db{l}"
+    for gi, (g, gg) in enumerate(zip(st.grids, gs.grids)):
+        if ktype == abi.NT_UNCONSTRAINED:
+            assert np.count_nonzero(g.grads) > 0
+            assert rel_err(to_np(gg.grads), g.grads) <= MLP_TOL, f"latent grad {gi}"
+            # texels the oracle leaves untouched stay exactly zero
+            assert np.all(to_np(gg.grads)[g.grads == 0] == 0)
+        elif ktype == abi.NT_BLOCK_FEATURES:
+            assert rel_err(to_np(gg.block_grads), g.block_grads) <= MLP_TOL, f"block grad {gi}"
+        else:
+            assert np.all(to_np(gg.block_grads) == 0)
+
+
+def test_train_step_accumulates(lib, O):
+    """Two passes without an optimizer step add up (the zero-gradient contract)."""
+    say("case: train accumulate")
+    st = make_state("c2", image=64, region=(32, 16), seed=4)
+    gs = gpu_workspace(lib, st.to_torch(), abi.NT_UNCONSTRAINED)
+    for _ in range(2):
+        assert O.ntref_train_step(C.byref(st.params()), 0, 1) == 0
+        nt.check(lib.nt_train_step(C.byref(gs.params()), 0, None))
+    sync()
+    assert rel_err(to_np(gs.net.weight_grads[1]), st.net.weight_grads[1]) <= MLP_TOL
+    assert rel_err(to_np(gs.grids[0].grads), st.grids[0].grads) <= MLP_TOL
+
+
+# ---- Adam ------------------------------------------------------------------------------------
+
+def test_optimize_network_and_latents_bit_exact(lib, O):
+    say("case: adam network + latents")
+    rng = np.random.default_rng(40)
+    st = make_state("c2", image=64, region=(32, 16), seed=5, step=3)
+    for l in range(st.net.num_layers):
+        g = st.net.weight_grads[l]
+        g[:] = np.where(rng.uniform(size=g.size) < 0.7, rng.normal(0, 1e-3, g.size), 0)
+        st.net.weight_moment1[l][:] = rng.normal(0, 1e-4, g.size)
+        st.net.weight_moment2[l][:] = rng.uniform(0, 1e-6, g.size)
+        st.net.bias_grads[l][:] = rng.normal(0, 1e-3, st.net.bias_grads[l].size)
+    for g in st.grids:
+        g.grads[:] = np.where(rng.uniform(size=g.grads.size) < 0.3, rng.normal(0, 1e-2, g.grads.size), 0)
+        g.moment1[:] = rng.normal(0, 1e-3, g.grads.size)
+        g.moment2[:] = rng.uniform(0, 1e-4, g.grads.size)
+    gs = st.to_torch()
+    assert O.ntref_optimize_network(C.byref(st.params())) == 0
+    assert O.ntref_optimize_latents(C.byref(st.params()), 0) == 0
+    nt.check(lib.nt_optimize_network(C.byref(gs.params()), None))
+    nt.check(lib.nt_optimize_latents(C.byref(gs.params()), 0, None))
+    sync()
+    for l in range(st.net.num_layers):
+        for name in ("weights", "weight_grads", "weight_moment1", "weight_moment2", "biases",
+                     "bias_grads", "bias_moment1", "bias_moment2"):
+            a, b = to_np(getattr(gs.net, name)[l]), getattr(st.net, name)[l]
+            assert np.array_equal(a.view(np.uint16) if a.dtype == np.int16 else a, b), (name, l)
+    for g, gg in zip(st.grids, gs.grids):
+        for name in ("values", "grads", "moment1", "moment2"):
+            assert np.array_equal(to_np(getattr(gg, name)), getattr(g, name)), name
+
+
+def test_optimize_block_latents(lib, O):
+    say("case: adam blocks")
+    rng = np.random.default_rng(41)
+    st = make_state("ref", image=64, region=(32, 16), seed=6, step=2, blocks=True)
+    for g in st.grids:
+        g.block_grads[:] = np.where(rng.uniform(size=g.block_grads.size) < 0.5,
+                                    rng.normal(0, 1e-2, g.block_grads.size), 0)
+    gs = st.to_torch()
+    assert O.ntref_optimize_latents(C.byref(st.params()), abi.NT_BLOCK_FEATURES) == 0
+    nt.check(lib.nt_optimize_latents(C.byref(gs.params()), abi.NT_BLOCK_FEATURES, None))
+    sync()
+    for g, gg in zip(st.grids, gs.grids):
+        assert np.array_equal(to_np(gg.block_params), g.block_params)
+        assert np.array_equal(to_np(gg.block_grads), g.block_grads)
+
+
+# ---- inference (train.cu:917-961) --------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", ["ref", "c2"])
+def test_inference(lib, O, shape):
+    import torch
+    say(f"case: inference {shape}")
+    st = make_state(shape, image=48, region=(16, 16), seed=7)
+    no = st.net.sizes[-1]
+    st.inference_output = np.zeros(48 * 48 * no, np.float32)
+    st.inference_mse_accum = np.zeros(1, np.float32)
+    gs = st.to_torch()
+    assert O.ntref_inference(C.byref(st.params())) == 0
+    nt.check(lib.nt_inference(C.byref(gs.params()), None))
+    sync()
+    assert rel_err(to_np(gs.inference_output), st.inference_output) <= MLP_TOL
+    assert abs(float(to_np(gs.inference_mse_accum)[0]) - float(st.inference_mse_accum[0])) <= \
+        1e-2 * abs(float(st.inference_mse_accum[0]))
+
+
+# ---- codec ----------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("w,h,c", [(64, 64, 16), (37, 22, 16), (16, 8, 8), (9, 13, 4), (20, 12, 12)])
+def test_codec_bit_exact(lib, O, w, h, c):
+    import torch
+    say(f"case: codec {w}x{h}x{c}")
+    rng = np.random.default_rng(w * h + c)
+    vals = rng.normal(0, 0.5, size=w * h * c).astype(np.float32)
+    vals[:7] = [0.0, -0.0, 1e-8, -1e-8, 7e4, -7e4, 65504.0]
+    nb = ((w + 3) // 4) * ((h + 3) // 4) * 12 * c
+    want = np.zeros(nb, np.uint8)
+    assert O.ntref_codec_encode(vals.ctypes.data, w, h, c, want.ctypes.data) == 0
+    gv = torch.from_numpy(vals).cuda()
+    gb = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+    nt.check(lib.nt_codec_encode(gv.data_ptr(), w, h, c, gb.data_ptr(), None))
+    sync()
+    assert np.array_equal(gb.cpu().numpy(), want)
+    dec = np.zeros(w * h * c, np.float32)
+    assert O.ntref_codec_decode(want.ctypes.data, w, h, c, dec.ctypes.data) == 0
+    gd = torch.zeros(w * h * c, dtype=torch.float32, device="cuda")
+    nt.check(lib.nt_codec_decode(gb.data_ptr(), w, h, c, gd.data_ptr(), None))
+    sync()
+    assert np.array_equal(gd.cpu().numpy().view(np.uint32), dec.view(np.uint32))
+
+
+# ---- decode from quantized latents ------------------------------------------------------------------
+
+def test_decode_from_codec_latents(lib, O):
+    import torch
+    say("case: decode c4")
+    rng = np.random.default_rng(50)
+    C16 = 16
+    sizes = [(64, 5), (32, 5), (16, 4), (8, 3)]
+    blobs, grids_np = [], []
+    for size, mips in sizes:
+        offs, total = P.codec_chain_layout(size, size, mips, C16)
+        blob = np.zeros(total, np.uint8)
+        for m in range(mips):
+            s = P.mip_dim(size, m)
+            vals = rng.normal(0, 0.5, size=s * s * C16).astype(np.float32)
+            blk = np.zeros(((s + 3) // 4) ** 2 * 12 * C16, np.uint8)
+            assert O.ntref_codec_encode(vals.ctypes.data, s, s, C16, blk.ctypes.data) == 0
+            blob[offs[m]:offs[m] + blk.size] = blk
+        blobs.append((size, mips, offs, blob))
+    net = P.make_network([64, 64, 64, 64, 12], rng=rng, init="xavier")
+    W = H = 96
+
+    def dparams(blob_ptrs, netv, out_ptr):
+        d = abi.nt_decode_params()
+        d.num_grids, d.channels = 4, C16
+        for i, (size, mips, offs, _) in enumerate(blobs):
+            d.grids[i].width = d.grids[i].height = size
+            d.grids[i].num_mips = mips
+            for m, o in enumerate(offs):
+                d.grids[i].byte_offset[m] = o
+            d.grids[i].blocks = blob_ptrs[i]
+        d.mlp = netv.struct()
+        d.out_width, d.out_height = W, H
+        d.seed, d.jitter, d.mip_min, d.mip_max = 1234, 1.0, 0.0, 3.0
+        d.output = C.cast(out_ptr, abi.u16p)
+        return d
+
+    want = np.zeros(W * H * 12, np.uint16)
+    dp = dparams([b[3].ctypes.data for b in blobs], net, want.ctypes.data)
+    assert O.ntref_decode(C.byref(dp), 1) == 0
+    gblobs = [torch.from_numpy(b[3]).cuda() for b in blobs]
+    gnet = net.converted(True, "cuda")
+    gout = torch.zeros(W * H * 12, dtype=torch.int16, device="cuda")
+    gp = dparams([g.data_ptr() for g in gblobs], gnet, gout.data_ptr())
+    nt.check(lib.nt_decode(C.byref(gp), None))
+    sync()
+    got = gout.cpu().numpy().view(np.float16).astype(np.float32)
+    assert rel_err(got, want.view(np.float16).astype(np.float32)) <= MLP_TOL

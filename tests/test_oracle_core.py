@@ -1,0 +1,266 @@
+"""Pins the CPU oracle's scalar pieces: fp16 arithmetic, the RNG, sample positions, latent
+and texture filtering, target packing. Each check is independent of the oracle's own code
+(numpy's IEEE conversions, published constants, textbook filter kernels, brute force).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from neural_textures_amd import abi, params as P
+from oracle_lib import load_oracle
+
+O = load_oracle()
+
+
+# ---- fp16 ----------------------------------------------------------------------------
+
+def test_f16_to_f32_exhaustive():
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([O.ntref_f16_to_f32(int(b)) for b in bits], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_ieee_round_nearest_even():
+    rng = np.random.default_rng(1)
+    x = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    edge = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 2**-24, 2**-25, 1.5 * 2**-25,
+                     2**-14, 2**-14 - 2**-25, 1.0 + 2**-11, 1.0 + 3 * 2**-11, np.inf, -np.inf],
+                    np.float32)
+    x = np.concatenate([x[~np.isnan(x)], edge])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    got = np.array([O.ntref_f32_to_f16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f16_add_is_correctly_rounded():
+    rng = np.random.default_rng(2)
+    a = rng.integers(0, 0x7C00, size=50_000).astype(np.uint16) | (rng.integers(0, 2, 50_000) << 15).astype(np.uint16)
+    b = rng.integers(0, 0x7C00, size=50_000).astype(np.uint16) | (rng.integers(0, 2, 50_000) << 15).astype(np.uint16)
+    exact = a.view(np.float16).astype(np.float64) + b.view(np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):
+        want = exact.astype(np.float16).view(np.uint16)  # numpy rounds double -> half directly
+    got = np.array([O.ntref_f16_add(int(x), int(y)) for x, y in zip(a, b)], np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---- RNG and sample positions (train.cu:37-58, 827-844) -------------------------------
+
+def test_xorshift32_known_answers():
+    s = C.c_uint32(1)
+    assert [O.ntref_xorshift32(C.byref(s)) for _ in range(3)] == [270369, 67634689, 2647435461]
+
+
+def test_sample_seed_and_first_uniforms():
+    seed = O.ntref_sample_seed(0, 0)
+    assert seed == 2891336453
+    assert O.ntref_sample_seed(0 ^ 2891336453, 0) == 1  # a zero seed becomes 1
+    s = C.c_uint32(seed)
+    u0, u1 = O.ntref_uniform(C.byref(s)), O.ntref_uniform(C.byref(s))
+    assert abs(u0 - 0.9293574095) < 1e-9 and abs(u1 - 0.3933818936) < 1e-9
+
+
+def test_sample_position_region_and_clamp():
+    st = P.TrainState([P.make_grid(8, 8, 1, 3)], P.make_network([3, 16, 16]), [], 64, 32,
+                      num_samples=64 * 4, region_width=64, texel_offset_x=0, texel_offset_y=30)
+    p = st.params()
+    uvz = (C.c_float * 3)()
+    for i in [0, 63, 64, 200, 255]:
+        O.ntref_sample_uvz(C.byref(p), i, uvz)
+        x = (i % 64) + 0.5
+        y = 30 + (i // 64) + 0.5
+        assert abs(uvz[0] * 64 - x) <= 0.5 + 1e-5 and 0.5 / 64 - 1e-7 <= uvz[0] <= 1 - 0.5 / 64 + 1e-7
+        assert uvz[1] * 32 <= 31.5 + 1e-5  # clamped to the image (train.cu:838-841)
+        assert abs(uvz[1] * 32 - min(y, 31.5)) <= 0.5 + 1e-5
+        assert uvz[2] == 0.0
+
+
+# ---- latent bilinear sampling (train.cu:263-314) --------------------------------------
+
+def _lat(grids):
+    lat = abi.nt_latents()
+    lat.num_grids, lat.channels = len(grids), grids[0].channels
+    for i, g in enumerate(grids):
+        lat.grids[i] = g.struct()
+    return lat
+
+
+def _sample(lat, u, v, z, n):
+    out = (C.c_uint16 * n)()
+    O.ntref_sample_latents_bilinear(C.byref(lat), (C.c_float * 3)(u, v, z), out)
+    return np.frombuffer(out, np.uint16).view(np.float16).astype(np.float64)
+
+
+def _bilinear64(img, u, v):
+    """Textbook bilinear with wrap addressing in float64; img [h, w, c]."""
+    h, w, _ = img.shape
+    tu, tv = u * w - 0.5, v * h - 0.5
+    x0, y0 = int(np.floor(tu)), int(np.floor(tv))
+    fx, fy = tu - x0, tv - y0
+    acc = 0.0
+    for cy, wy in ((0, 1 - fy), (1, fy)):
+        for cx, wx in ((0, 1 - fx), (1, fx)):
+            acc = acc + wx * wy * img[(y0 + cy) % h, (x0 + cx) % w].astype(np.float64)
+    return acc
+
+
+def test_bilinear_texel_centre_is_exact():
+    rng = np.random.default_rng(3)
+    g = P.make_grid(16, 8, 1, 3, rng)
+    lat = _lat([g])
+    img = g.mip(g.values, 0)
+    for x, y in [(0, 0), (5, 3), (15, 7)]:
+        got = _sample(lat, (x + 0.5) / 16, (y + 0.5) / 8, 0.0, 3)
+        assert np.array_equal(got, img[y, x].astype(np.float16).astype(np.float64))
+
+
+def test_bilinear_matches_textbook_with_wrap():
+    rng = np.random.default_rng(4)
+    g = P.make_grid(16, 16, 1, 8, rng)
+    lat = _lat([g])
+    img = g.mip(g.values, 0)
+    for u, v in list(rng.uniform(0, 1, size=(200, 2))) + [(0.001, 0.999), (0.999, 0.001), (0.0, 0.0)]:
+        got = _sample(lat, u, v, 0.0, 8)
+        want = _bilinear64(img, np.float32(u), np.float32(v))
+        # four fp16 roundings of |contribution| <= 1 and four fp16 adds
+        assert np.max(np.abs(got - want)) < 4e-3
+
+
+def test_trilinear_blends_two_mips():
+    rng = np.random.default_rng(5)
+    g = P.make_grid(16, 16, 3, 3, rng)
+    lat = _lat([g])
+    for u, v, z in [(0.3, 0.6, 0.25), (0.8, 0.1, 1.5), (0.5, 0.5, 2.0), (0.2, 0.2, 7.3)]:
+        got = _sample(lat, u, v, z, 3)
+        m0 = min(int(np.floor(z)), 2)
+        m1 = min(m0 + 1, 2)
+        f = z - np.floor(z)
+        want = (1 - f) * _bilinear64(g.mip(g.values, m0), u, v)
+        if f > 0:
+            want = want + f * _bilinear64(g.mip(g.values, m1), u, v)
+        assert np.max(np.abs(got - want)) < 8e-3
+
+
+def test_scatter_is_adjoint_of_bilinear_sample():
+    """<sample(L), g> == <L, scatter(g)> (train.cu:460-509 vs 263-314), float64 reference."""
+    rng = np.random.default_rng(6)
+    grids = [P.make_grid(8, 8, 2, 3, rng), P.make_grid(4, 4, 2, 3, rng)]
+    lat = _lat(grids)
+    for _ in range(20):
+        u, v = rng.uniform(0, 1, 2)
+        gvec = rng.uniform(-1, 1, 6).astype(np.float16)
+        for g in grids:
+            g.grads[:] = 0
+        O.ntref_scatter_unconstrained(C.byref(lat), (C.c_float * 3)(u, v, 0.0),
+                                      gvec.view(np.uint16).ctypes.data_as(C.POINTER(C.c_uint16)))
+        lhs = sum(float(np.dot(_bilinear64(g.mip(g.values, 0), np.float32(u), np.float32(v)),
+                               gvec[3 * i:3 * i + 3].astype(np.float64))) for i, g in enumerate(grids))
+        rhs = sum(float(np.dot(g.values.astype(np.float64), g.grads.astype(np.float64))) for g in grids)
+        assert abs(lhs - rhs) < 1e-5 * max(1.0, abs(lhs))
+
+
+# ---- Catmull-Rom (filter/catmull_rom.h:37-89) -----------------------------------------
+
+def _cr_kernel(x):
+    """Textbook Catmull-Rom kernel (cubic convolution, a = -0.5)."""
+    x = abs(x)
+    if x <= 1:
+        return 1.5 * x**3 - 2.5 * x**2 + 1
+    if x < 2:
+        return -0.5 * x**3 + 2.5 * x**2 - 4 * x + 2
+    return 0.0
+
+
+def test_catmull_rom_weights_match_textbook_kernel():
+    w = (C.c_float * 4)()
+    for f in np.linspace(0, 1, 101, dtype=np.float32):
+        O.ntref_catmull_rom_weights(float(f), w)
+        f = float(f)
+        want = [_cr_kernel(1 + f), _cr_kernel(f), _cr_kernel(1 - f), _cr_kernel(2 - f)]
+        assert np.allclose(list(w), want, atol=2e-7)
+        assert abs(sum(w) - 1.0) < 1e-6
+    O.ntref_catmull_rom_weights(0.0, w)
+    assert list(w) == [0.0, 1.0, 0.0, 0.0]
+
+
+def _texture(data, nch):
+    t = P.make_texture(data.shape[1], data.shape[0], nch, data)
+    return t, t.struct()
+
+
+def _tex_sample(ts, u, v, z=0.0):
+    out = (C.c_float * 4)()
+    O.ntref_sample_texture(C.byref(ts), u, v, z, out)
+    return np.array(list(out))
+
+
+def test_catmull_rom_reproduces_linear_ramps():
+    H = W = 32
+    yy, xx = np.mgrid[0:H, 0:W].astype(np.float64)
+    data = np.stack([0.25 + 0.01 * xx + 0.02 * yy, 1.0 - 0.005 * xx, 0.5 + 0.003 * yy,
+                     np.zeros_like(xx)], -1).astype(np.float32)
+    t, ts = _texture(data, 3)
+    rng = np.random.default_rng(7)
+    for u, v in rng.uniform(0.15, 0.85, size=(100, 2)).astype(np.float32):
+        s, r = u * W - 0.5, v * H - 0.5  # texel-space coordinate
+        want = [0.25 + 0.01 * s + 0.02 * r, 1.0 - 0.005 * s, 0.5 + 0.003 * r]
+        assert np.allclose(_tex_sample(ts, u, v)[:3], want, atol=2e-5)
+
+
+def test_catmull_rom_16_taps_equal_reference_9_taps_with_exact_bilinear():
+    """The reference fetches 9 bilinear taps with merged middle weights
+    (catmull_rom.h:61-86); with exact bilinear filtering that equals the 16-tap filter."""
+    rng = np.random.default_rng(8)
+    H, W = 16, 24
+    data = rng.uniform(0, 1, size=(H, W, 4)).astype(np.float32)
+    t, ts = _texture(data, 4)
+
+    def bil(x, y):  # exact bilinear at texel-space (x, y) with wrap (HW linear filter)
+        x0, y0 = int(np.floor(x - 0.5)), int(np.floor(y - 0.5))
+        fx, fy = x - 0.5 - x0, y - 0.5 - y0
+        acc = np.zeros(4)
+        for cy, wy in ((0, 1 - fy), (1, fy)):
+            for cx, wx in ((0, 1 - fx), (1, fx)):
+                acc += wx * wy * data[(y0 + cy) % H, (x0 + cx) % W]
+        return acc
+
+    for u, v in rng.uniform(0, 1, size=(100, 2)):
+        sx, sy = u * W, v * H
+        p1x, p1y = np.floor(sx - 0.5) + 0.5, np.floor(sy - 0.5) + 0.5
+        fx, fy = sx - p1x, sy - p1y
+        wx = [_cr_kernel(1 + fx), _cr_kernel(fx), _cr_kernel(1 - fx), _cr_kernel(2 - fx)]
+        wy = [_cr_kernel(1 + fy), _cr_kernel(fy), _cr_kernel(1 - fy), _cr_kernel(2 - fy)]
+        w12x, w12y = wx[1] + wx[2], wy[1] + wy[2]
+        px = [p1x - 1, p1x + wx[2] / w12x, p1x + 2]
+        py = [p1y - 1, p1y + wy[2] / w12y, p1y + 2]
+        wxs, wys = [wx[0], w12x, wx[3]], [wy[0], w12y, wy[3]]
+        want = sum(bil(px[i], py[j]) * wxs[i] * wys[j] for j in range(3) for i in range(3))
+        got = _tex_sample(ts, np.float32(u), np.float32(v))
+        assert np.allclose(got, want, atol=3e-6)
+
+
+def test_target_packing_follows_reference_rules():
+    """1-channel textures give one output; others min(ch, 4) (train.cu:105-157)."""
+    rng = np.random.default_rng(9)
+    H = W = 8
+    specs = [(3, 1.0), (1, 4.0), (4, 2.0), (2, 0.5)]
+    textures = []
+    for nch, lw in specs:
+        d = rng.uniform(0, 1, size=(H, W, 4)).astype(np.float32)
+        t = P.make_texture(W, H, nch, d, loss_weight=lw)
+        textures.append(t)
+    st = P.TrainState([P.make_grid(4, 4, 1, 3)], P.make_network([3, 16, 16]), textures, W, H, 1)
+    p = st.params()
+    exp, wts = (C.c_float * 16)(), (C.c_float * 16)()
+    uvz = (C.c_float * 3)(0.37, 0.61, 0.0)
+    n = O.ntref_expected_values(C.byref(p), uvz, exp, wts)
+    assert n == 3 + 1 + 4 + 2
+    assert list(wts)[:n] == [1.0] * 3 + [4.0] + [2.0] * 4 + [0.5] * 2
+    assert list(wts)[n:] == [1.0] * (16 - n) and list(exp)[n:] == [0.0] * (16 - n)
+    per_tex = [_tex_sample(t.struct(), 0.37, 0.61) for t in textures]
+    want = list(per_tex[0][:3]) + [per_tex[1][0]] + list(per_tex[2][:4]) + list(per_tex[3][:2])
+    assert np.allclose(list(exp)[:n], want, atol=0)
