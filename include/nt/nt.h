@@ -201,6 +201,12 @@ int64_t nt_block_chain_layout(int width, int height, int num_mips, int64_t *bloc
 /* Bytes of scratch nt_train_step needs for these parameters (0 on error). */
 size_t nt_train_workspace_bytes(const nt_params *params, nt_kernel_type type);
 
+/* Profiling hook (no reference counterpart): the next nt_train_step, nt_optimize_latents,
+ * nt_inference, nt_forward, nt_mlp_forward, nt_decode, nt_codec_encode or nt_codec_decode
+ * on this thread records `start` right before and `stop` right after its main kernel, on
+ * that call's stream. Both are hipEvent_t passed as void*; NULL clears. One-shot. */
+int nt_profile_next_launch(void *start_event, void *stop_event);
+
 /* ---- the hot path ----------------------------------------------------------------- */
 
 /*

@@ -17,6 +17,27 @@ using namespace ntk;
 namespace {
 
 thread_local char g_error[512] = "";
+thread_local hipEvent_t g_prof_start = nullptr;
+thread_local hipEvent_t g_prof_stop = nullptr;
+
+// Brackets one kernel launch with the one-shot profiling events, if set.
+struct ProfileScope {
+    hipStream_t s;
+    hipEvent_t stop;
+    explicit ProfileScope(hipStream_t stream) : s(stream), stop(g_prof_stop)
+    {
+        if (g_prof_start && g_prof_stop)
+            hipEventRecord(g_prof_start, s);
+        else
+            stop = nullptr;
+        g_prof_start = g_prof_stop = nullptr;
+    }
+    ~ProfileScope()
+    {
+        if (stop)
+            hipEventRecord(stop, s);
+    }
+};
 
 int fail(int status, const char *fmt, ...)
 {
@@ -232,8 +253,10 @@ int pack_targets(const nt_texture *tex, int ntex, int8_t *out_tex, int8_t *out_c
 
 struct TrainPlan {
     int shape, nwg, chunks_per_wg, tiles_x, P, stage1_blocks, rows_per_block;
-    int fp_floats;
+    int fp_floats, fp_stride, tile_ok, scatter_mfma, w_rows, union_off;
+    size_t weight_bytes;
     int fp_w[NT_MAX_GRIDS], fp_h[NT_MAX_GRIDS], fp_off[NT_MAX_GRIDS];
+    int cb_w[NT_MAX_GRIDS], cb_h[NT_MAX_GRIDS], w_row0[NT_MAX_GRIDS];
     size_t lds, workspace;
 };
 
@@ -275,23 +298,60 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->P = train_grad_total(shape);
     plan->rows_per_block = 32;
     plan->stage1_blocks = (plan->nwg + plan->rows_per_block - 1) / plan->rows_per_block;
-    plan->workspace = ((size_t)plan->nwg + (size_t)plan->stage1_blocks) * (size_t)plan->P * sizeof(float);
+    plan->weight_bytes = train_weight_bytes(shape);
+    plan->workspace = plan->weight_bytes +
+                      ((size_t)plan->nwg + (size_t)plan->stage1_blocks) * (size_t)plan->P * sizeof(float);
 
-    // LDS footprint box per grid: every texel a 64 x 8 block of positions can touch.
+    // LDS footprint box per grid: every texel a 64 x 8 block of positions can touch (the
+    // bilinear corners of positions in [x, x + 64] span at most ceil(64 r) + 2 texels, plus
+    // one of rounding slack on each side). Texels are `fp_stride` (odd) floats apart so
+    // that neighbouring texels fall in different LDS banks.
     const int C = p->latents.channels;
-    size_t lds = train_lds_static(shape);
-    int fp = 0;
+    plan->fp_stride = C | 1;
+    int fp = 0, w_rows = 0;
     for (int gi = 0; gi < p->latents.num_grids; ++gi) {
         const nt_grid &g = p->latents.grids[gi];
-        plan->fp_w[gi] = (int)std::ceil((double)tile_w * g.width / p->image_width) + 5;
-        plan->fp_h[gi] = (int)std::ceil((double)kChunkH * g.height / p->image_height) + 5;
+        const double rx = (double)g.width / p->image_width, ry = (double)g.height / p->image_height;
+        plan->fp_w[gi] = (int)std::ceil(tile_w * rx) + 4;
+        plan->fp_h[gi] = (int)std::ceil(kChunkH * ry) + 4;
         plan->fp_off[gi] = fp;
-        fp += plan->fp_w[gi] * plan->fp_h[gi] * C;
+        fp += plan->fp_w[gi] * plan->fp_h[gi] * plan->fp_stride;
+        // Chunk cell box for the MFMA scatter: positions in [x, x + 16] x [y, y + 8].
+        plan->cb_w[gi] = (int)std::ceil(kChunkW * rx) + 2;
+        plan->cb_h[gi] = (int)std::ceil(kChunkH * ry) + 2;
+        plan->w_row0[gi] = w_rows;
+        w_rows += 16 * ((plan->cb_w[gi] * plan->cb_h[gi] + 15) / 16);
     }
-    plan->fp_floats = fp;
-    if (type != NT_UNCONSTRAINED || lds + (size_t)fp * 4 > kMaxLds)
-        plan->fp_floats = 0; // scatter straight to global memory
-    plan->lds = lds + (size_t)plan->fp_floats * 4;
+    plan->w_rows = w_rows;
+    // The chunk's target taps are staged in LDS when every reference texture has the image
+    // size (as the reference requires, main.cpp:972-978).
+    plan->tile_ok = p->num_textures > 0;
+    for (int ti = 0; ti < p->num_textures && ti < NT_MAX_TEXTURES; ++ti) {
+        const nt_texture &t = p->textures[ti];
+        if (t.texels && t.num_channels > 0 && (t.width != p->image_width || t.height != p->image_height))
+            plan->tile_ok = 0;
+    }
+    const size_t head = train_lds_static(shape);
+    const size_t transposes = train_xt_bytes(shape);
+    const size_t tile = (size_t)p->num_textures * kTileW * kTileH * 16;
+    const size_t scatter = ((size_t)pad16(p->mlp.sizes[0]) + 2 * (size_t)w_rows) * kRowStride * 2;
+    auto total = [&](int fp_floats, bool use_tile, bool use_scatter) {
+        size_t un = transposes;
+        if (use_tile && tile > un)
+            un = tile;
+        if (use_scatter && scatter > un)
+            un = scatter;
+        return head + (((size_t)fp_floats * 4 + 15) & ~(size_t)15) + un;
+    };
+    plan->fp_floats = type == NT_UNCONSTRAINED ? fp : 0;
+    if (plan->fp_floats && total(plan->fp_floats, false, false) > kMaxLds)
+        plan->fp_floats = 0; // box does not fit: scatter straight to global memory
+    if (plan->tile_ok && total(plan->fp_floats, true, false) > kMaxLds)
+        plan->tile_ok = 0;
+    plan->scatter_mfma = plan->fp_floats > 0 && C == 16 &&
+                         total(plan->fp_floats, plan->tile_ok, true) <= kMaxLds;
+    plan->union_off = (int)(head + (((size_t)plan->fp_floats * 4 + 15) & ~(size_t)15));
+    plan->lds = total(plan->fp_floats, plan->tile_ok, plan->scatter_mfma);
     return NT_OK;
 }
 
@@ -324,6 +384,13 @@ const char *nt_status_string(int status)
 }
 
 const char *nt_last_error(void) { return g_error; }
+
+int nt_profile_next_launch(void *start_event, void *stop_event)
+{
+    g_prof_start = (hipEvent_t)start_event;
+    g_prof_stop = (hipEvent_t)stop_event;
+    return NT_OK;
+}
 
 int64_t nt_mip_chain_layout(int width, int height, int num_mips, int64_t *mip_offset)
 {
@@ -386,6 +453,9 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
         d.grid[gi].fp_w = plan.fp_w[gi];
         d.grid[gi].fp_h = plan.fp_h[gi];
         d.grid[gi].fp_off = plan.fp_off[gi];
+        d.grid[gi].cb_w = plan.cb_w[gi];
+        d.grid[gi].cb_h = plan.cb_h[gi];
+        d.grid[gi].w_row0 = plan.w_row0[gi];
     }
     const int nout = pack_targets(p->textures, p->num_textures, d.out_tex, d.out_ch, d.out_w, d.tex);
     if (nout < 0)
@@ -403,10 +473,29 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     d.tiles_x = plan.tiles_x;
     d.chunks_per_wg = plan.chunks_per_wg;
     d.fp_floats = plan.fp_floats;
-    d.partial = (float *)p->workspace;
+    d.fp_stride = plan.fp_stride;
+    d.tile_ok = plan.tile_ok;
+    d.scatter_mfma = plan.scatter_mfma;
+    d.w_rows = plan.w_rows;
+    d.union_off = plan.union_off;
+    // Workspace: weight fragments | fp32 biases | per-workgroup partials | reduction rows.
+    uint8_t *ws = (uint8_t *)p->workspace;
+    PrepDesc prep{};
+    prep.mlp = d.mlp;
+    prep.frags = (uint4 *)ws;
+    prep.bias = (float *)(ws + train_frag_bytes(plan.shape));
+    d.wfrags = prep.frags;
+    d.wbias = prep.bias;
+    d.partial = (float *)(ws + plan.weight_bytes);
 
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = launch_train(plan.shape, type, d, plan.nwg, plan.lds, s);
+    hipError_t e = launch_prep_weights(plan.shape, prep, s);
+    if (e != hipSuccess)
+        return hip_status(e, "weight preparation launch");
+    {
+        ProfileScope prof(s);
+        e = launch_train(plan.shape, type, d, plan.nwg, plan.lds, s);
+    }
     if (e != hipSuccess)
         return hip_status(e, "train kernel launch");
 
@@ -542,6 +631,7 @@ int nt_optimize_latents(const nt_params *p, nt_kernel_type type, void *stream)
         }
     }
     d.start[lat.num_grids] = start;
+    ProfileScope prof((hipStream_t)stream);
     return hip_status(launch_latent_adam(d, (hipStream_t)stream), "latent Adam launch");
 }
 
@@ -594,6 +684,7 @@ int nt_inference(const nt_params *p, void *stream)
     d.out32 = p->inference_output;
     d.sse = p->inference_mse_accum;
     d.out_stride = p->mlp.sizes[p->mlp.num_layers];
+    ProfileScope prof((hipStream_t)stream);
     return hip_status(launch_forward(shape, kFwdInference, d, (hipStream_t)stream), "inference launch");
 }
 
@@ -614,6 +705,7 @@ int nt_mlp_forward(const nt_mlp *mlp, const uint16_t *inputs, uint16_t *outputs,
     d.inputs = inputs;
     d.out16 = outputs;
     d.out_stride = mlp->sizes[mlp->num_layers];
+    ProfileScope prof((hipStream_t)stream);
     return hip_status(launch_forward(shape, kFwdMlp, d, (hipStream_t)stream), "MLP forward launch");
 }
 
@@ -639,6 +731,7 @@ int nt_forward(const nt_latents *latents, const nt_mlp *mlp, nt_filter filter, c
     d.out16 = outputs;
     d.out_stride = mlp->sizes[mlp->num_layers];
     const int mode = filter == NT_FILTER_BILINEAR ? kFwdBilinear : kFwdCatmullRom;
+    ProfileScope prof((hipStream_t)stream);
     return hip_status(launch_forward(shape, mode, d, (hipStream_t)stream), "forward launch");
 }
 
@@ -674,6 +767,7 @@ int nt_codec_encode(const float *values, int width, int height, int channels, vo
                     channels);
     if (((uintptr_t)blocks & 3u) || ((uintptr_t)values & 3u))
         return fail(NT_ERR_MISALIGNED, "values/blocks must be 4-byte aligned");
+    ProfileScope prof((hipStream_t)stream);
     return hip_status(launch_codec_encode(values, width, height, channels, (uint8_t *)blocks, (hipStream_t)stream),
                       "codec encode launch");
 }
@@ -687,6 +781,7 @@ int nt_codec_decode(const void *blocks, int width, int height, int channels, flo
                     channels);
     if (!aligned16(blocks) || !aligned16(values))
         return fail(NT_ERR_MISALIGNED, "values/blocks must be 16-byte aligned");
+    ProfileScope prof((hipStream_t)stream);
     return hip_status(
         launch_codec_decode((const uint8_t *)blocks, width, height, channels, values, (hipStream_t)stream),
         "codec decode launch");
@@ -742,6 +837,7 @@ int nt_decode(const nt_decode_params *p, void *stream)
     d.jitter = p->jitter;
     d.mip_min = p->mip_min;
     d.mip_max = p->mip_max;
+    ProfileScope prof((hipStream_t)stream);
     return hip_status(launch_forward(shape, kFwdDecode, d, (hipStream_t)stream), "decode launch");
 }
 

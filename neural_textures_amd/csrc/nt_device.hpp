@@ -24,6 +24,17 @@ __device__ __forceinline__ f16v mfma32(h8 a, h8 b, f16v c)
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// An fp32 value rounded and materialised as fp32. The backend otherwise folds
+// (half)(a * b) and (half)(h + a * b) into v_fma_mix*_f16 with a single rounding, while the
+// reference computes the fp32 product (and sum) first and rounds to fp16 afterwards.
+__device__ __forceinline__ float rn32(float x)
+{
+    asm volatile("" : "+v"(x));
+    return x;
+}
+// fp32 -> fp16 of an fp32 product, with the product rounded to fp32 first.
+__device__ __forceinline__ _Float16 half_of_product(float a, float b) { return (_Float16)rn32(a * b); }
+
 __device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)bits_h(b); }

@@ -66,14 +66,14 @@ __device__ __forceinline__ void sample_bilinear(const FwdDesc &d, float u, float
                     const float4 *p = (const float4 *)(vals + ((int64_t)ty * w + tx) * C);
                     const float4 a = p[0], b = p[1];
                     const float wc = f.w[c];
-                    x[q][0] = x[q][0] + (_Float16)(wc * a.x);
-                    x[q][1] = x[q][1] + (_Float16)(wc * a.y);
-                    x[q][2] = x[q][2] + (_Float16)(wc * a.z);
-                    x[q][3] = x[q][3] + (_Float16)(wc * a.w);
-                    x[q][4] = x[q][4] + (_Float16)(wc * b.x);
-                    x[q][5] = x[q][5] + (_Float16)(wc * b.y);
-                    x[q][6] = x[q][6] + (_Float16)(wc * b.z);
-                    x[q][7] = x[q][7] + (_Float16)(wc * b.w);
+                    x[q][0] = x[q][0] + half_of_product(wc, a.x);
+                    x[q][1] = x[q][1] + half_of_product(wc, a.y);
+                    x[q][2] = x[q][2] + half_of_product(wc, a.z);
+                    x[q][3] = x[q][3] + half_of_product(wc, a.w);
+                    x[q][4] = x[q][4] + half_of_product(wc, b.x);
+                    x[q][5] = x[q][5] + half_of_product(wc, b.y);
+                    x[q][6] = x[q][6] + half_of_product(wc, b.z);
+                    x[q][7] = x[q][7] + half_of_product(wc, b.w);
                 }
             }
         } else {
@@ -95,7 +95,7 @@ __device__ __forceinline__ void sample_bilinear(const FwdDesc &d, float u, float
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         const int tx = wrap_coord(f.x0 + (c & 1), w), ty = wrap_coord(f.y0 + (c >> 1), h);
-                        a = a + (_Float16)(f.w[c] * vals[((int64_t)ty * w + tx) * C + ch]);
+                        a = a + half_of_product(f.w[c], vals[((int64_t)ty * w + tx) * C + ch]);
                     }
                 }
                 x[q][e] = a;
@@ -178,7 +178,7 @@ __device__ __forceinline__ void sample_codec(const FwdDesc &d, float u, float v,
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float val = codec_value(ends[e] & 0xFFFFu, ends[e] >> 16, (idx >> (4 * e)) & 15);
-                    x[q][e] = x[q][e] + (_Float16)(wc * val);
+                    x[q][e] = x[q][e] + half_of_product(wc, val);
                 }
             }
         }

@@ -18,6 +18,11 @@ constexpr int kChunkH = 8;
 constexpr int kChunk = kChunkW * kChunkH;
 constexpr int kTrainThreads = 256;
 constexpr int kRowStride = kChunk + 8; // fp16 row stride of the LDS transposes
+// Catmull-Rom target tile of one chunk: texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of every
+// reference texture, float4 each (covers all 16 taps of every jittered sample of the chunk).
+constexpr int kTileX0 = 3;
+constexpr int kTileW = kChunkW + 7;
+constexpr int kTileH = kChunkH + 7;
 
 // One latent grid at the mip levels a kernel samples.
 struct GridDesc {
@@ -27,6 +32,7 @@ struct GridDesc {
     float *block_grads;
     int w, h, num_mips;
     int fp_w, fp_h, fp_off; // train kernel: LDS footprint box and offset (floats)
+    int cb_w, cb_h, w_row0; // train kernel: chunk cell box and its first row in the scatter matrices
     int64_t mip_off[NT_MAX_MIPS];   // texels
     int64_t block_off[NT_MAX_MIPS]; // blocks
 };
@@ -48,8 +54,22 @@ struct TrainDesc {
     int image_w, image_h, off_x, off_y, region_w, num_samples;
     uint32_t step;
     int tiles_x, chunks_per_wg;
-    int fp_floats; // LDS footprint floats (0: scatter straight to global)
+    int fp_floats;  // LDS footprint floats (0: scatter straight to global)
+    int fp_stride;  // floats per texel in the footprint box (odd: spreads texels over banks)
+    int tile_ok;    // the chunk's target taps are staged in LDS (textures match the image size)
+    int scatter_mfma; // latent scatter as an MFMA reduction over the chunk (else LDS atomics)
+    int w_rows;     // rows of each bilinear-weight matrix (all grids, 16-row tiles)
+    int union_off;  // byte offset of the LDS region shared by tile / transposes / scatter
+    const uint4 *wfrags; // weight fragments in LDS order, prepared by prep_weights
+    const float *wbias;
     float *partial; // [gridDim.x][grad_total] per-workgroup MLP gradient partials
+};
+
+// Weight-fragment preparation (once per train step) for the train kernel.
+struct PrepDesc {
+    MlpDesc mlp;
+    uint4 *frags;
+    float *bias;
 };
 
 // Gradient reduction descriptor: partial[rows][P] -> mlp gradients.
@@ -132,6 +152,10 @@ enum ShapeId {
 hipError_t launch_train(int shape, int type, const TrainDesc &d, int num_wg, size_t lds,
                         hipStream_t s);
 size_t train_lds_static(int shape);
+size_t train_xt_bytes(int shape);
+size_t train_weight_bytes(int shape);
+size_t train_frag_bytes(int shape);
+hipError_t launch_prep_weights(int shape, const PrepDesc &d, hipStream_t s);
 int train_grad_total(int shape);
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s);
 hipError_t launch_forward(int shape, int mode, const FwdDesc &d, hipStream_t s);

@@ -90,58 +90,71 @@ struct MlpDesc {
     int num_layers;
 };
 
-// Stage forward and backward weight fragments and fp32 biases in LDS. All threads of the
-// block take part; the caller synchronises afterwards.
+// Element idx = fragment * 64 + lane of the forward/backward weight fragments, in the
+// order layer_forward / layer_backward_dx read them.
+template <class S>
+__device__ h8 weight_fragment(const MlpDesc &m, int idx)
+{
+    const int f = idx / kWave, lane = idx % kWave, c = lane & 31, g = lane >> 5;
+    h8 v;
+    int l = 0;
+    const bool fwd = f < S::fwd_total();
+    if (fwd) {
+        while (l + 1 < S::L && f >= S::fwd_off(l + 1))
+            ++l;
+    } else {
+        while (l + 1 < S::L && f >= S::bwd_off(l + 1))
+            ++l;
+    }
+    const int kin = S::kin(l), kout = S::kout(l);
+    const uint16_t *W = m.W[l];
+    if (fwd) {
+        // Forward fragment (a, q) of layer l, lane (c, g), element e: W_l[k][n] with
+        // n = 32a + c and k the layer's input feature for (q, g, e).
+        const int local = f - S::fwd_off(l), qn = kin / 16;
+        const int a = local / qn, q = local % qn;
+        const int n = 32 * a + c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = l == 0 ? natural_feature(q, g, e) : chained_feature(q, g, e);
+            v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+        }
+    } else {
+        // Backward (dX) fragment (m, q) of layer l: A[k][kk] = W_l[k][n], k = 32m + c,
+        // n = chained output feature of (q, g, e).
+        const int local = f - S::bwd_off(l), qn = kout / 16;
+        const int mt = local / qn, q = local % qn;
+        const int k = 32 * mt + c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int n = chained_feature(q, g, e);
+            v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+        }
+    }
+    return v;
+}
+
+// fp32 bias row idx (layers back to back, each padded to 32-row tiles).
+template <class S>
+__device__ float bias_value(const MlpDesc &m, int idx)
+{
+    int l = 0;
+    while (l + 1 < S::L && idx >= S::bias_off(l + 1))
+        ++l;
+    const int n = idx - S::bias_off(l);
+    return n < m.sizes[l + 1] ? h2f(m.B[l][n]) : 0.f;
+}
+
+// Stage forward (and, unless FWD_ONLY, backward) weight fragments and fp32 biases in LDS.
+// All threads of the block take part; the caller synchronises afterwards.
 template <class S, bool FWD_ONLY = false>
 __device__ void stage_weights(const MlpDesc &m, h8 *frags, float *bias, int tid, int nthreads)
 {
     constexpr int nfrags = FWD_ONLY ? S::fwd_total() : S::all_frags();
-    // Forward fragment (a, q) of layer l, lane (c, g), element e: W_l[k][n] with
-    // n = 32a + c and k the layer's input feature for (q, g, e).
-    for (int idx = tid; idx < nfrags * kWave; idx += nthreads) {
-        const int f = idx / kWave, lane = idx % kWave, c = lane & 31, g = lane >> 5;
-        h8 v;
-        int l = 0;
-        bool fwd = f < S::fwd_total();
-        if (fwd) {
-            while (l + 1 < S::L && f >= S::fwd_off(l + 1))
-                ++l;
-        } else {
-            while (l + 1 < S::L && f >= S::bwd_off(l + 1))
-                ++l;
-        }
-        const int kin = S::kin(l), kout = S::kout(l);
-        const uint16_t *W = m.W[l];
-        if (fwd) {
-            const int local = f - S::fwd_off(l), qn = kin / 16;
-            const int a = local / qn, q = local % qn;
-            const int n = 32 * a + c;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int k = l == 0 ? natural_feature(q, g, e) : chained_feature(q, g, e);
-                v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
-            }
-        } else {
-            // Backward (dX) fragment (m, q) of layer l: A[k][kk] = W_l[k][n], k = 32m + c,
-            // n = chained output feature of (q, g, e).
-            const int local = f - S::bwd_off(l), qn = kout / 16;
-            const int mt = local / qn, q = local % qn;
-            const int k = 32 * mt + c;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int n = chained_feature(q, g, e);
-                v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
-            }
-        }
-        frags[idx] = v;
-    }
-    for (int idx = tid; idx < S::bias_total(); idx += nthreads) {
-        int l = 0;
-        while (l + 1 < S::L && idx >= S::bias_off(l + 1))
-            ++l;
-        const int n = idx - S::bias_off(l);
-        bias[idx] = n < m.sizes[l + 1] ? h2f(m.B[l][n]) : 0.f;
-    }
+    for (int idx = tid; idx < nfrags * kWave; idx += nthreads)
+        frags[idx] = weight_fragment<S>(m, idx);
+    for (int idx = tid; idx < S::bias_total(); idx += nthreads)
+        bias[idx] = bias_value<S>(m, idx);
 }
 
 // One forward layer for one 32-sample tile: acc[a] = bias + W^T x.

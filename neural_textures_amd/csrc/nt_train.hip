@@ -25,9 +25,10 @@ struct TrainLayout {
     static constexpr int max_out = S::H > S::OUT ? S::H : S::OUT;
     static constexpr int xt_rows = 32 * S::t32(max_in);
     static constexpr int dyt_rows = 32 * S::t32(max_out);
-    static constexpr int xt_off = frag_bytes + bias_bytes;
-    static constexpr int dyt_off = xt_off + xt_rows * kRowStride * 2;
-    static constexpr int fp_off = dyt_off + dyt_rows * kRowStride * 2;
+    // LDS: weight fragments | fp32 biases | latent footprint box (runtime size) | a union of
+    // the chunk's target tile, the layer transposes and the scatter matrices (runtime size).
+    static constexpr int head_bytes = frag_bytes + bias_bytes;
+    static constexpr int transpose_bytes = (xt_rows + dyt_rows) * kRowStride * 2;
     static constexpr int slots = (S::dw_total() + 3) / 4;
 };
 
@@ -84,6 +85,13 @@ __device__ __forceinline__ const GridDesc &grid_ref(const TrainDesc &d, int gi)
     return d.grid[gi];
 }
 
+// Wrap for coordinates within one period of the image: training positions are clamped into
+// the image (train.cu:838-841), so every bilinear corner lies in [-1, size].
+__device__ __forceinline__ int wrap_near(int c, int size)
+{
+    return c < 0 ? c + size : (c >= size ? c - size : c);
+}
+
 // Unconstrained latent gather into natural-layout B fragments: lane group g of a sample
 // holds features 16q + 8g + e. Corner contributions are rounded to fp16 and summed in
 // fp16, corner by corner (train.cu:293-310).
@@ -110,19 +118,19 @@ __device__ __forceinline__ void gather_unconstrained(const TrainDesc &d, const S
                 const int gh = C == 16 ? d.grid[q].h : (g ? d.grid[(2 * q + 1) & 3].h : d.grid[2 * q].h);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const int tx = wrap_coord(x0 + (c & 1), gw);
-                    const int ty = wrap_coord(y0 + (c >> 1), gh);
+                    const int tx = wrap_near(x0 + (c & 1), gw);
+                    const int ty = wrap_near(y0 + (c >> 1), gh);
                     const float4 *p = (const float4 *)(vals + ((int64_t)ty * gw + tx) * C + cb);
                     const float4 a = p[0], b = p[1];
                     const float wc = w[c];
-                    acc[0] = acc[0] + (_Float16)(wc * a.x);
-                    acc[1] = acc[1] + (_Float16)(wc * a.y);
-                    acc[2] = acc[2] + (_Float16)(wc * a.z);
-                    acc[3] = acc[3] + (_Float16)(wc * a.w);
-                    acc[4] = acc[4] + (_Float16)(wc * b.x);
-                    acc[5] = acc[5] + (_Float16)(wc * b.y);
-                    acc[6] = acc[6] + (_Float16)(wc * b.z);
-                    acc[7] = acc[7] + (_Float16)(wc * b.w);
+                    acc[0] = acc[0] + half_of_product(wc, a.x);
+                    acc[1] = acc[1] + half_of_product(wc, a.y);
+                    acc[2] = acc[2] + half_of_product(wc, a.z);
+                    acc[3] = acc[3] + half_of_product(wc, a.w);
+                    acc[4] = acc[4] + half_of_product(wc, b.x);
+                    acc[5] = acc[5] + half_of_product(wc, b.y);
+                    acc[6] = acc[6] + half_of_product(wc, b.z);
+                    acc[7] = acc[7] + half_of_product(wc, b.w);
                 }
             }
         } else {
@@ -138,9 +146,9 @@ __device__ __forceinline__ void gather_unconstrained(const TrainDesc &d, const S
                     _Float16 a = (_Float16)0.f;
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const int tx = wrap_coord(x0 + (c & 1), gr.w);
-                        const int ty = wrap_coord(y0 + (c >> 1), gr.h);
-                        a = a + (_Float16)(w[c] * gr.values[((int64_t)ty * gr.w + tx) * C + ch]);
+                        const int tx = wrap_near(x0 + (c & 1), gr.w);
+                        const int ty = wrap_near(y0 + (c >> 1), gr.h);
+                        a = a + half_of_product(w[c], gr.values[((int64_t)ty * gr.w + tx) * C + ch]);
                     }
                     acc[e] = a;
                 }
@@ -195,7 +203,7 @@ __device__ __forceinline__ void gather_bc6(const TrainDesc &d, const SampleFootp
                     const float v = bc6_decompress(rec[2 * t.part * C + ch],
                                                    rec[(2 * t.part + 1) * C + ch], t.bits,
                                                    rec[4 * C + t.pix]);
-                    a = (_Float16)((float)a + w[c] * v);
+                    a = (_Float16)rn32((float)a + rn32(w[c] * v));
                 }
             }
             x[q][e] = a;
@@ -247,6 +255,102 @@ __device__ __forceinline__ void lane_targets(const TrainDesc &d, float u, float 
                         acc[3] = fmaf(p.w, wxy, acc[3]);
                 } else {
                     acc[0] = fmaf(tx.texels[base], wxy, acc[0]);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if (oti[e] == ti) {
+                const int c = och[e];
+                t[e] = c == 0 ? acc[0] : c == 1 ? acc[1] : c == 2 ? acc[2] : acc[3];
+            }
+        }
+    }
+}
+
+// Stage the chunk's Catmull-Rom footprint of every reference texture in LDS: texels
+// [cx0 - kTileX0, cx0 - kTileX0 + kTileW) x [cy0 - kTileX0, ... + kTileH), float4 each,
+// wrapped like the reference's texture objects (main.cpp:613-621).
+__device__ __forceinline__ void load_target_tile(const TrainDesc &d, float4 *tile, int cx0, int cy0,
+                                                 int tid)
+{
+    constexpr int per = kTileW * kTileH;
+    for (int i = tid; i < d.ntex * per; i += kTrainThreads) {
+        const int t = i / per, r = i % per;
+        const int ty = r / kTileW, tx = r % kTileW;
+        const TexDesc &tex = d.tex[t];
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tex.texels) {
+            const int gx = wrap_coord(cx0 - kTileX0 + tx, tex.w);
+            const int gy = wrap_coord(cy0 - kTileX0 + ty, tex.h);
+            const int64_t base = (int64_t)gy * tex.w + gx;
+            if (tex.pitch == 4)
+                v = *(const float4 *)(tex.texels + base * 4);
+            else
+                v.x = tex.texels[base];
+        }
+        tile[i] = v;
+    }
+}
+
+// Catmull-Rom targets for the lane's eight output rows from the staged tile: the same taps,
+// weights and fp32 fma order as lane_targets (train.cu:105-157).
+__device__ __forceinline__ void lane_targets_tile(const TrainDesc &d, const float4 *tile, int cx0,
+                                                  int cy0, float u, float v, int g, float (&t)[8],
+                                                  float (&wt)[8])
+{
+    int oti[8], och[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int o = chained_feature(0, g, e);
+        oti[e] = d.out_tex[o];
+        och[e] = d.out_ch[o];
+        wt[e] = d.out_w[o];
+        t[e] = 0.f;
+    }
+    float wx[4], wy[4];
+    const int x0 = cr_axis(u, d.image_w, wx) - (cx0 - kTileX0);
+    const int y0 = cr_axis(v, d.image_h, wy) - (cy0 - kTileX0);
+    const bool inside = x0 >= 0 && x0 + 3 < kTileW && y0 >= 0 && y0 + 3 < kTileH;
+    for (int ti = 0; ti < d.ntex; ++ti) {
+        bool need = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            need |= oti[e] == ti;
+        if (!need)
+            continue;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (inside) {
+            const float4 *base = tile + ti * (kTileW * kTileH) + y0 * kTileW + x0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 p = base[j * kTileW + i];
+                    const float wxy = wx[i] * wy[j];
+                    acc[0] = fmaf(p.x, wxy, acc[0]);
+                    acc[1] = fmaf(p.y, wxy, acc[1]);
+                    acc[2] = fmaf(p.z, wxy, acc[2]);
+                    acc[3] = fmaf(p.w, wxy, acc[3]);
+                }
+        } else {
+            const TexDesc tx = d.tex[ti];
+            const int gx0 = x0 + (cx0 - kTileX0), gy0 = y0 + (cy0 - kTileX0);
+            for (int j = 0; j < 4; ++j) {
+                const int y = wrap_coord(gy0 + j, tx.h);
+                for (int i = 0; i < 4; ++i) {
+                    const int x = wrap_coord(gx0 + i, tx.w);
+                    const float wxy = wx[i] * wy[j];
+                    const int64_t b = ((int64_t)y * tx.w + x) * tx.pitch;
+                    if (tx.pitch == 4) {
+                        const float4 p = *(const float4 *)(tx.texels + b);
+                        acc[0] = fmaf(p.x, wxy, acc[0]);
+                        acc[1] = fmaf(p.y, wxy, acc[1]);
+                        acc[2] = fmaf(p.z, wxy, acc[2]);
+                        acc[3] = fmaf(p.w, wxy, acc[3]);
+                    } else {
+                        acc[0] = fmaf(tx.texels[b], wxy, acc[0]);
+                    }
                 }
             }
         }
@@ -356,9 +460,9 @@ __device__ __forceinline__ void scatter_unconstrained(const TrainDesc &d, const 
                 const int tx = x0 + (c & 1), ty = y0 + (c >> 1);
                 const int lx = tx - lox, ly = ty - loy;
                 if (d.fp_floats > 0 && lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h) {
-                    lds_add(fp + gr.fp_off + (ly * gr.fp_w + lx) * C + ch, val);
+                    lds_add(fp + gr.fp_off + (ly * gr.fp_w + lx) * d.fp_stride + ch, val);
                 } else {
-                    const int wx = wrap_coord(tx, gr.w), wy = wrap_coord(ty, gr.h);
+                    const int wx = wrap_near(tx, gr.w), wy = wrap_near(ty, gr.h);
                     global_add(gr.grads + ((int64_t)wy * gr.w + wx) * C + ch, val);
                 }
             }
@@ -406,6 +510,133 @@ __device__ __forceinline__ void scatter_bc6(const TrainDesc &d, const SampleFoot
         }
 }
 
+__device__ __forceinline__ f4v mfma16(h8 a, h8 b, f4v c)
+{
+    // D(16x16) += A(16x32) B(32x16): lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16],
+    // D[4(l/16)+r][l%16].
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Latent gradient scatter of one 128-sample chunk as an MFMA reduction over the samples
+// (train.cu:460-509 without atomics): per grid, the chunk's cell box gradient is
+//   D[cell][ch] = sum_s W[cell][s] * dX0[s][ch],
+// W holding each sample's four bilinear corner weights (fp32 split into fp16 hi + lo, so
+// the products equal the reference's fp32 weight * fp16 gradient to ~2^-22). D is added
+// into the workgroup footprint box by the one lane that owns each (cell, channel).
+// Corners outside the chunk box (fp32 rounding at the box edge) go to the box by atomics.
+template <class S, int C>
+__device__ __forceinline__ void scatter_mfma(const TrainDesc &d, const SampleFootprints &f,
+                                             const h8 (&dx)[S::K0 / 16], bool valid, int cx0, int cy0,
+                                             const int (&flo_x)[NT_MAX_GRIDS],
+                                             const int (&flo_y)[NT_MAX_GRIDS], float *fp,
+                                             unsigned char *un, int col, int wave, int lane, int tid)
+{
+    static_assert(C == 16, "grid g's channels are rows [16g, 16g + 16) of the dX0 transpose");
+    constexpr int KQ0 = S::K0 / 16;
+    _Float16 *dxt = (_Float16 *)un;
+    _Float16 *whi = dxt + S::K0 * kRowStride;
+    _Float16 *wlo = whi + d.w_rows * kRowStride;
+    const int g = lane >> 5;
+    {
+        uint4 *z = (uint4 *)whi;
+        const int n = 2 * d.w_rows * kRowStride / 8;
+        for (int i = tid; i < n; i += kTrainThreads)
+            z[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    store_transposed<KQ0, true>(dxt, dx, col, g);
+    int cbx0[NT_MAX_GRIDS], cby0[NT_MAX_GRIDS];
+#pragma unroll
+    for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
+        const GridDesc &gr = d.grid[gi];
+        cbx0[gi] = (int)floorf((float)cx0 * (float)gr.w / (float)d.image_w - 0.5f);
+        cby0[gi] = (int)floorf((float)cy0 * (float)gr.h / (float)d.image_h - 0.5f);
+    }
+    __syncthreads();
+    if (valid) {
+#pragma unroll
+        for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
+            if (gi >= d.G)
+                break;
+            const GridDesc &gr = d.grid[gi];
+#pragma unroll
+            for (int corner = 0; corner < 4; ++corner) {
+                const int tx = f.x0[gi] + (corner & 1), ty = f.y0[gi] + (corner >> 1);
+                const int cx = tx - cbx0[gi], cy = ty - cby0[gi];
+                const float w = f.w[gi][corner];
+                if (cx >= 0 && cx < gr.cb_w && cy >= 0 && cy < gr.cb_h) {
+                    if ((corner >> 1) == g) {
+                        const int row = gr.w_row0 + cy * gr.cb_w + cx;
+                        const _Float16 hi = (_Float16)w;
+                        whi[row * kRowStride + col] = hi;
+                        wlo[row * kRowStride + col] = (_Float16)(w - (float)hi);
+                    }
+                } else {
+                    const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
+                    const bool inbox = lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h;
+#pragma unroll
+                    for (int q = 0; q < KQ0; ++q)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int feat = chained_feature(q, g, e);
+                            if (feat / C != gi)
+                                continue;
+                            const int ch = feat % C;
+                            const float val = w * (float)dx[q][e];
+                            if (inbox)
+                                lds_add(fp + gr.fp_off + (ly * gr.fp_w + lx) * d.fp_stride + ch, val);
+                            else
+                                global_add(gr.grads + ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * C + ch, val);
+                        }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // One task per (grid, 16-row tile of its cells), spread over the waves.
+    int task = 0;
+#pragma unroll
+    for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
+        if (gi >= d.G)
+            break;
+        const GridDesc &gr = d.grid[gi];
+        const int ncell = gr.cb_w * gr.cb_h;
+        const int ntile = (ncell + 15) >> 4;
+        for (int t = 0; t < ntile; ++t, ++task) {
+            if ((task & 3) != wave)
+                continue;
+            f4v acc = {0.f, 0.f, 0.f, 0.f};
+            const _Float16 *ah = whi + (gr.w_row0 + 16 * t + (lane & 15)) * kRowStride + 8 * (lane >> 4);
+            const _Float16 *al = wlo + (gr.w_row0 + 16 * t + (lane & 15)) * kRowStride + 8 * (lane >> 4);
+            const _Float16 *bp = dxt + (gi * C + (lane & 15)) * kRowStride + 8 * (lane >> 4);
+#pragma unroll
+            for (int k = 0; k < kChunk / 32; ++k) {
+                const h8 b = *(const h8 *)(bp + 32 * k);
+                acc = mfma16(*(const h8 *)(ah + 32 * k), b, acc);
+                acc = mfma16(*(const h8 *)(al + 32 * k), b, acc);
+            }
+            const int ch = lane & 15;
+            if (ch < C) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int cell = 16 * t + 4 * (lane >> 4) + r;
+                    if (cell >= ncell || acc[r] == 0.f)
+                        continue;
+                    const int tx = cbx0[gi] + cell % gr.cb_w, ty = cby0[gi] + cell / gr.cb_w;
+                    const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
+                    if (lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h) {
+                        float *p = fp + gr.fp_off + (ly * gr.fp_w + lx) * d.fp_stride + ch;
+                        *p += acc[r];
+                    } else {
+                        global_add(gr.grads + ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * C + ch,
+                                   acc[r]);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Backward through hidden layer l (its input is hidden activation l-1), then l-1 ... 1.
 template <class S, int l>
 __device__ __forceinline__ void backward_hidden(_Float16 *xt, _Float16 *dyt, const h8 *frags,
@@ -443,14 +674,22 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
     extern __shared__ __align__(16) unsigned char smem[];
     h8 *frags = (h8 *)smem;
     float *bias = (float *)(smem + LY::frag_bytes);
-    _Float16 *xt = (_Float16 *)(smem + LY::xt_off);
-    _Float16 *dyt = (_Float16 *)(smem + LY::dyt_off);
-    float *fp = (float *)(smem + LY::fp_off);
+    float *fp = (float *)(smem + LY::head_bytes);
+    unsigned char *un = smem + d.union_off;
+    _Float16 *xt = (_Float16 *)un;
+    _Float16 *dyt = xt + LY::xt_rows * kRowStride;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
-    stage_weights<S>(d.mlp, frags, bias, tid, kTrainThreads);
+    {
+        uint4 *dst = (uint4 *)frags;
+        for (int i = tid; i < S::all_frags() * kWave; i += kTrainThreads)
+            dst[i] = d.wfrags[i];
+        for (int i = tid; i < S::bias_total(); i += kTrainThreads)
+            bias[i] = d.wbias[i];
+    }
     for (int i = tid; i < d.fp_floats; i += kTrainThreads)
         fp[i] = 0.f;
+    float4 *tile = (float4 *)un; // aliases the transposes: used before them in every chunk
 
     const int tile_x = blockIdx.x % d.tiles_x, tile_y = blockIdx.x / d.tiles_x;
     const int tx0 = tile_x * kChunkW * d.chunks_per_wg, ty0 = tile_y * kChunkH;
@@ -477,6 +716,11 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 
     const int col = 32 * wave + c; // column of this lane's sample in the LDS transposes
     for (int chunk = 0; chunk < d.chunks_per_wg; ++chunk) {
+        const int cx0 = d.off_x + tx0 + chunk * kChunkW, cy0 = d.off_y + ty0;
+        if (d.tile_ok) {
+            load_target_tile(d, tile, cx0, cy0, tid);
+            __syncthreads();
+        }
         // ---- sample position (train.cu:827-844)
         const int sx = tx0 + chunk * kChunkW + (c & 15);
         const int sy = ty0 + 2 * wave + (c >> 4);
@@ -506,7 +750,12 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
                 x0[q] = (h8)(_Float16)0.f;
         }
         float tgt[8], tw[8];
-        lane_targets(d, u, v, g, tgt, tw);
+        if (d.tile_ok) {
+            lane_targets_tile(d, tile, cx0, cy0, u, v, g, tgt, tw);
+            __syncthreads(); // the transposes below overwrite the tile
+        } else {
+            lane_targets(d, u, v, g, tgt, tw);
+        }
 
         // ---- forward (mlp.h:65-99)
         h8 xh[NH][HQ];
@@ -577,8 +826,16 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 
         // ---- latent gradient scatter
         if constexpr (TYPE == NT_UNCONSTRAINED) {
-            if (valid)
-                scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
+            if constexpr (C == 16) {
+                if (d.scatter_mfma)
+                    scatter_mfma<S, C>(d, fps, dx0, valid, cx0, cy0, flo_x, flo_y, fp, un, col, wave,
+                                       lane, tid);
+                else if (valid)
+                    scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
+            } else {
+                if (valid)
+                    scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
+            }
         } else if constexpr (TYPE == NT_BLOCK_FEATURES) {
             if (valid)
                 scatter_bc6<C, KQ0>(d, fps, dx0, g);
@@ -599,9 +856,18 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
                     gi = k;
             const GridDesc &gr = d.grid[gi];
             const int local = i - gr.fp_off;
-            const int ch = local % C, cell = local / C;
+            const int ch = local % d.fp_stride, cell = local / d.fp_stride;
+            if (ch >= C)
+                continue;
             const int lx = cell % gr.fp_w, ly = cell / gr.fp_w;
-            const int wx = wrap_coord(flo_x[gi] + lx, gr.w), wy = wrap_coord(flo_y[gi] + ly, gr.h);
+            int lox = flo_x[0], loy = flo_y[0];
+#pragma unroll
+            for (int k = 1; k < NT_MAX_GRIDS; ++k)
+                if (gi == k) {
+                    lox = flo_x[k];
+                    loy = flo_y[k];
+                }
+            const int wx = wrap_coord(lox + lx, gr.w), wy = wrap_coord(loy + ly, gr.h);
             global_add(gr.grads + ((int64_t)wy * gr.w + wx) * C + ch, val);
         }
     }
@@ -685,6 +951,28 @@ __global__ __launch_bounds__(256) void reduce_stage2(ReduceDesc d)
     }
 }
 
+// Weight fragments and fp32 biases in the train kernel's LDS order, computed once per step
+// so that every workgroup stages them with plain 16-byte copies.
+template <class S>
+__global__ __launch_bounds__(256) void prep_weights_kernel(PrepDesc d)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < S::all_frags() * kWave) {
+        const h8 v = weight_fragment<S>(d.mlp, i);
+        d.frags[i] = __builtin_bit_cast(uint4, v);
+    }
+    if (i < S::bias_total())
+        d.bias[i] = bias_value<S>(d.mlp, i);
+}
+
+template <class S>
+static hipError_t launch_prep(const PrepDesc &d, hipStream_t s)
+{
+    const int n = S::all_frags() * kWave > S::bias_total() ? S::all_frags() * kWave : S::bias_total();
+    hipLaunchKernelGGL(prep_weights_kernel<S>, dim3((n + 255) / 256), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s)
 {
     dim3 g1((d.P + 255) / 256, d.stage1_blocks);
@@ -740,15 +1028,77 @@ hipError_t launch_train(int shape, int type, const TrainDesc &d, int num_wg, siz
     }
 }
 
+hipError_t launch_prep_weights(int shape, const PrepDesc &d, hipStream_t s)
+{
+    switch (shape) {
+    case kShapeRef:
+        return launch_prep<ShapeRef>(d, s);
+    case kShapeC2:
+        return launch_prep<ShapeC2>(d, s);
+    case kShapeC4:
+        return launch_prep<ShapeC4>(d, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+template <class S>
+static size_t weight_bytes()
+{
+    return (size_t)S::all_frags() * kWave * 16 + (((size_t)S::bias_total() * 4 + 255) / 256) * 256;
+}
+
+size_t train_weight_bytes(int shape)
+{
+    switch (shape) {
+    case kShapeRef:
+        return weight_bytes<ShapeRef>();
+    case kShapeC2:
+        return weight_bytes<ShapeC2>();
+    case kShapeC4:
+        return weight_bytes<ShapeC4>();
+    default:
+        return 0;
+    }
+}
+
+size_t train_frag_bytes(int shape)
+{
+    switch (shape) {
+    case kShapeRef:
+        return (size_t)ShapeRef::all_frags() * kWave * 16;
+    case kShapeC2:
+        return (size_t)ShapeC2::all_frags() * kWave * 16;
+    case kShapeC4:
+        return (size_t)ShapeC4::all_frags() * kWave * 16;
+    default:
+        return 0;
+    }
+}
+
+size_t train_xt_bytes(int shape)
+{
+    switch (shape) {
+    case kShapeRef:
+        return TrainLayout<ShapeRef>::transpose_bytes;
+    case kShapeC2:
+        return TrainLayout<ShapeC2>::transpose_bytes;
+    case kShapeC4:
+        return TrainLayout<ShapeC4>::transpose_bytes;
+    default:
+        return 0;
+    }
+}
+
 size_t train_lds_static(int shape)
 {
     switch (shape) {
     case kShapeRef:
-        return TrainLayout<ShapeRef>::fp_off;
+        return TrainLayout<ShapeRef>::head_bytes;
     case kShapeC2:
-        return TrainLayout<ShapeC2>::fp_off;
+        return TrainLayout<ShapeC2>::head_bytes;
     case kShapeC4:
-        return TrainLayout<ShapeC4>::fp_off;
+        return TrainLayout<ShapeC4>::head_bytes;
     default:
         return 0;
     }
