@@ -270,6 +270,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true", help="skip decode and codec")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="first run one device-to-device copy of BYTES (a known-size kernel for "
+                         "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the path "
@@ -283,6 +286,14 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     lib = nt.load()
     ev = HipEvents()
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe // 4, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: copy probe of {args.copy_probe} bytes done")
+        del src, dst
 
     log("bench: config 2 train steps")
     st, ms_per_step, kernel_ms, kernel_med = bench_train(lib, nt, args, ev)

@@ -253,7 +253,7 @@ int pack_targets(const nt_texture *tex, int ntex, int8_t *out_tex, int8_t *out_c
 
 struct TrainPlan {
     int shape, nwg, chunks_per_wg, tiles_x, P, stage1_blocks, rows_per_block;
-    int fp_floats, fp_stride, tile_ok, scatter_mfma, w_rows, union_off;
+    int fp_floats, fp_stride, tile_ok, scatter_mfma, scatter_split, scatter_off, w_rows, union_off;
     size_t weight_bytes;
     int fp_w[NT_MAX_GRIDS], fp_h[NT_MAX_GRIDS], fp_off[NT_MAX_GRIDS];
     int cb_w[NT_MAX_GRIDS], cb_h[NT_MAX_GRIDS], w_row0[NT_MAX_GRIDS];
@@ -335,23 +335,38 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     const size_t transposes = train_xt_bytes(shape);
     const size_t tile = (size_t)p->num_textures * kTileW * kTileH * 16;
     const size_t scatter = ((size_t)pad16(p->mlp.sizes[0]) + 2 * (size_t)w_rows) * kRowStride * 2;
-    auto total = [&](int fp_floats, bool use_tile, bool use_scatter) {
+    auto fp_bytes = [](int fp_floats) { return ((size_t)fp_floats * 4 + 15) & ~(size_t)15; };
+    auto union_bytes = [&](bool use_tile, bool scatter_in_union) {
         size_t un = transposes;
         if (use_tile && tile > un)
             un = tile;
-        if (use_scatter && scatter > un)
+        if (scatter_in_union && scatter > un)
             un = scatter;
-        return head + (((size_t)fp_floats * 4 + 15) & ~(size_t)15) + un;
+        return un;
     };
     plan->fp_floats = type == NT_UNCONSTRAINED ? fp : 0;
-    if (plan->fp_floats && total(plan->fp_floats, false, false) > kMaxLds)
+    if (plan->fp_floats && head + fp_bytes(plan->fp_floats) + union_bytes(false, false) > kMaxLds)
         plan->fp_floats = 0; // box does not fit: scatter straight to global memory
-    if (plan->tile_ok && total(plan->fp_floats, true, false) > kMaxLds)
+    if (plan->tile_ok && head + fp_bytes(plan->fp_floats) + union_bytes(true, false) > kMaxLds)
         plan->tile_ok = 0;
-    plan->scatter_mfma = plan->fp_floats > 0 && C == 16 &&
-                         total(plan->fp_floats, plan->tile_ok, true) <= kMaxLds;
-    plan->union_off = (int)(head + (((size_t)plan->fp_floats * 4 + 15) & ~(size_t)15));
-    plan->lds = total(plan->fp_floats, plan->tile_ok, plan->scatter_mfma);
+    const size_t base = head + fp_bytes(plan->fp_floats);
+    plan->union_off = (int)base;
+    plan->scatter_mfma = 0;
+    plan->scatter_split = 0;
+    plan->scatter_off = 0;
+    plan->lds = base + union_bytes(plan->tile_ok, false);
+    if (plan->fp_floats > 0 && C == 16) {
+        // The scatter matrices get their own region when it fits, which lets the scatter
+        // share the layer-0 dW phase; otherwise they reuse the union after that phase.
+        if (base + union_bytes(plan->tile_ok, false) + scatter <= kMaxLds) {
+            plan->scatter_mfma = plan->scatter_split = 1;
+            plan->scatter_off = (int)(base + union_bytes(plan->tile_ok, false));
+            plan->lds = plan->scatter_off + scatter;
+        } else if (base + union_bytes(plan->tile_ok, true) <= kMaxLds) {
+            plan->scatter_mfma = 1;
+            plan->lds = base + union_bytes(plan->tile_ok, true);
+        }
+    }
     return NT_OK;
 }
 
@@ -478,6 +493,8 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     d.scatter_mfma = plan.scatter_mfma;
     d.w_rows = plan.w_rows;
     d.union_off = plan.union_off;
+    d.scatter_split = plan.scatter_split;
+    d.scatter_off = plan.scatter_off;
     // Workspace: weight fragments | fp32 biases | per-workgroup partials | reduction rows.
     uint8_t *ws = (uint8_t *)p->workspace;
     PrepDesc prep{};

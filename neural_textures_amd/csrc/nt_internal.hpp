@@ -59,7 +59,9 @@ struct TrainDesc {
     int tile_ok;    // the chunk's target taps are staged in LDS (textures match the image size)
     int scatter_mfma; // latent scatter as an MFMA reduction over the chunk (else LDS atomics)
     int w_rows;     // rows of each bilinear-weight matrix (all grids, 16-row tiles)
-    int union_off;  // byte offset of the LDS region shared by tile / transposes / scatter
+    int union_off;  // byte offset of the LDS region shared by tile / transposes (/ scatter)
+    int scatter_split; // the scatter matrices have their own LDS region (at scatter_off)
+    int scatter_off;
     const uint4 *wfrags; // weight fragments in LDS order, prepared by prep_weights
     const float *wbias;
     float *partial; // [gridDim.x][grad_total] per-workgroup MLP gradient partials

@@ -33,17 +33,20 @@ struct TrainLayout {
 };
 
 // Per-sample bilinear footprints at mip 0 for every grid (train.cu:284-303 with z = 0).
+// Sized for NT_MAX_GRIDS; with 16 channels the grid count is K0/16 and the unused entries
+// fold away.
 struct SampleFootprints {
     int x0[NT_MAX_GRIDS], y0[NT_MAX_GRIDS];
     float w[NT_MAX_GRIDS][4];
 };
 
+template <int GM>
 __device__ __forceinline__ void sample_footprints(const TrainDesc &d, float u, float v,
                                                   SampleFootprints &f)
 {
 #pragma unroll
     for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
-        if (gi < d.G) {
+        if (gi < GM && gi < d.G) {
             const Footprint t = bilinear_footprint(u, v, d.grid[gi].w, d.grid[gi].h, 1.f - 0.f);
             f.x0[gi] = t.x0;
             f.y0[gi] = t.y0;
@@ -60,6 +63,7 @@ __device__ __forceinline__ void sample_footprints(const TrainDesc &d, float u, f
 }
 
 // Select grid gi's footprint without dynamic register indexing.
+template <int GM = NT_MAX_GRIDS>
 __device__ __forceinline__ void pick_footprint(const SampleFootprints &f, int gi, int &x0,
                                                int &y0, float (&w)[4])
 {
@@ -69,7 +73,7 @@ __device__ __forceinline__ void pick_footprint(const SampleFootprints &f, int gi
     for (int c = 0; c < 4; ++c)
         w[c] = f.w[0][c];
 #pragma unroll
-    for (int k = 1; k < NT_MAX_GRIDS; ++k) {
+    for (int k = 1; k < GM; ++k) {
         if (gi == k) {
             x0 = f.x0[k];
             y0 = f.y0[k];
@@ -281,8 +285,9 @@ __device__ __forceinline__ void load_target_tile(const TrainDesc &d, float4 *til
         const TexDesc &tex = d.tex[t];
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (tex.texels) {
-            const int gx = wrap_coord(cx0 - kTileX0 + tx, tex.w);
-            const int gy = wrap_coord(cy0 - kTileX0 + ty, tex.h);
+            int gx = cx0 - kTileX0 + tx, gy = cy0 - kTileX0 + ty;
+            gx = (unsigned)gx < (unsigned)tex.w ? gx : wrap_coord(gx, tex.w);
+            gy = (unsigned)gy < (unsigned)tex.h ? gy : wrap_coord(gy, tex.h);
             const int64_t base = (int64_t)gy * tex.w + gx;
             if (tex.pitch == 4)
                 v = *(const float4 *)(tex.texels + base * 4);
@@ -518,86 +523,101 @@ __device__ __forceinline__ f4v mfma16(h8 a, h8 b, f4v c)
 }
 
 // Latent gradient scatter of one 128-sample chunk as an MFMA reduction over the samples
-// (train.cu:460-509 without atomics): per grid, the chunk's cell box gradient is
+// (train.cu:460-509 without atomics): per grid, the chunk's cell-box gradient is
 //   D[cell][ch] = sum_s W[cell][s] * dX0[s][ch],
 // W holding each sample's four bilinear corner weights (fp32 split into fp16 hi + lo, so
 // the products equal the reference's fp32 weight * fp16 gradient to ~2^-22). D is added
-// into the workgroup footprint box by the one lane that owns each (cell, channel).
-// Corners outside the chunk box (fp32 rounding at the box edge) go to the box by atomics.
-template <class S, int C>
-__device__ __forceinline__ void scatter_mfma(const TrainDesc &d, const SampleFootprints &f,
-                                             const h8 (&dx)[S::K0 / 16], bool valid, int cx0, int cy0,
-                                             const int (&flo_x)[NT_MAX_GRIDS],
-                                             const int (&flo_y)[NT_MAX_GRIDS], float *fp,
-                                             unsigned char *un, int col, int wave, int lane, int tid)
+// into the workgroup footprint box by the one lane that owns each (cell, channel). Corners
+// outside the chunk box (fp32 rounding at the box edge) go to the box with LDS atomics.
+// LDS: dxt [K0][kRowStride] fp16 | W hi [w_rows][kRowStride] | W lo [w_rows][kRowStride].
+
+// Chunk cell-box origin of every grid.
+template <int GM>
+__device__ __forceinline__ void chunk_box(const TrainDesc &d, int cx0, int cy0, int (&bx)[NT_MAX_GRIDS],
+                                          int (&by)[NT_MAX_GRIDS])
 {
-    static_assert(C == 16, "grid g's channels are rows [16g, 16g + 16) of the dX0 transpose");
-    constexpr int KQ0 = S::K0 / 16;
-    _Float16 *dxt = (_Float16 *)un;
-    _Float16 *whi = dxt + S::K0 * kRowStride;
-    _Float16 *wlo = whi + d.w_rows * kRowStride;
-    const int g = lane >> 5;
-    {
-        uint4 *z = (uint4 *)whi;
-        const int n = 2 * d.w_rows * kRowStride / 8;
-        for (int i = tid; i < n; i += kTrainThreads)
-            z[i] = make_uint4(0u, 0u, 0u, 0u);
-    }
-    store_transposed<KQ0, true>(dxt, dx, col, g);
-    int cbx0[NT_MAX_GRIDS], cby0[NT_MAX_GRIDS];
 #pragma unroll
     for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
         const GridDesc &gr = d.grid[gi];
-        cbx0[gi] = (int)floorf((float)cx0 * (float)gr.w / (float)d.image_w - 0.5f);
-        cby0[gi] = (int)floorf((float)cy0 * (float)gr.h / (float)d.image_h - 0.5f);
+        bx[gi] = gi < GM ? (int)floorf((float)cx0 * (float)gr.w / (float)d.image_w - 0.5f) : 0;
+        by[gi] = gi < GM ? (int)floorf((float)cy0 * (float)gr.h / (float)d.image_h - 0.5f) : 0;
     }
-    __syncthreads();
-    if (valid) {
+}
+
+__device__ __forceinline__ void zero_scatter_weights(const TrainDesc &d, _Float16 *sct, int tid, int k0)
+{
+    uint4 *z = (uint4 *)(sct + k0 * kRowStride);
+    const int n = 2 * d.w_rows * kRowStride / 8;
+    for (int i = tid; i < n; i += kTrainThreads)
+        z[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Part 1 (before a barrier): this lane's input gradient into dxt and its two corner weights
+// per grid into W (lane group g writes corners 2g, 2g+1); out-of-box corners by atomics.
+template <class S, int C, int GM>
+__device__ __forceinline__ void scatter_write(const TrainDesc &d, const SampleFootprints &f,
+                                              const h8 (&dx)[S::K0 / 16], bool valid,
+                                              const int (&cbx)[NT_MAX_GRIDS], const int (&cby)[NT_MAX_GRIDS],
+                                              const int (&flo_x)[NT_MAX_GRIDS],
+                                              const int (&flo_y)[NT_MAX_GRIDS], float *fp,
+                                              _Float16 *sct, int col, int g)
+{
+    static_assert(C == 16, "grid g's channels are rows [16g, 16g + 16) of the dX0 transpose");
+    constexpr int KQ0 = S::K0 / 16;
+    _Float16 *dxt = sct;
+    _Float16 *whi = dxt + S::K0 * kRowStride;
+    _Float16 *wlo = whi + d.w_rows * kRowStride;
+    store_transposed<KQ0, true>(dxt, dx, col, g);
+    if (!valid)
+        return;
 #pragma unroll
-        for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
-            if (gi >= d.G)
-                break;
-            const GridDesc &gr = d.grid[gi];
+    for (int gi = 0; gi < GM; ++gi) {
+        const GridDesc &gr = d.grid[gi];
 #pragma unroll
-            for (int corner = 0; corner < 4; ++corner) {
-                const int tx = f.x0[gi] + (corner & 1), ty = f.y0[gi] + (corner >> 1);
-                const int cx = tx - cbx0[gi], cy = ty - cby0[gi];
-                const float w = f.w[gi][corner];
-                if (cx >= 0 && cx < gr.cb_w && cy >= 0 && cy < gr.cb_h) {
-                    if ((corner >> 1) == g) {
-                        const int row = gr.w_row0 + cy * gr.cb_w + cx;
-                        const _Float16 hi = (_Float16)w;
-                        whi[row * kRowStride + col] = hi;
-                        wlo[row * kRowStride + col] = (_Float16)(w - (float)hi);
-                    }
-                } else {
-                    const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
-                    const bool inbox = lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h;
+        for (int corner = 0; corner < 4; ++corner) {
+            const int tx = f.x0[gi] + (corner & 1), ty = f.y0[gi] + (corner >> 1);
+            const int cx = tx - cbx[gi], cy = ty - cby[gi];
+            const float w = f.w[gi][corner];
+            if (cx >= 0 && cx < gr.cb_w && cy >= 0 && cy < gr.cb_h) {
+                if ((corner >> 1) == g) {
+                    const int row = gr.w_row0 + cy * gr.cb_w + cx;
+                    const _Float16 hi = (_Float16)w;
+                    whi[row * kRowStride + col] = hi;
+                    wlo[row * kRowStride + col] = (_Float16)(w - (float)hi);
+                }
+            } else {
+                const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
+                const bool inbox = lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h;
 #pragma unroll
-                    for (int q = 0; q < KQ0; ++q)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const int feat = chained_feature(q, g, e);
-                            if (feat / C != gi)
-                                continue;
-                            const int ch = feat % C;
-                            const float val = w * (float)dx[q][e];
-                            if (inbox)
-                                lds_add(fp + gr.fp_off + (ly * gr.fp_w + lx) * d.fp_stride + ch, val);
-                            else
-                                global_add(gr.grads + ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * C + ch, val);
-                        }
+                for (int e = 0; e < 8; ++e) {
+                    const int ch = chained_feature(0, g, e);
+                    const float val = w * (float)dx[gi][e];
+                    if (inbox)
+                        lds_add(fp + gr.fp_off + (ly * gr.fp_w + lx) * d.fp_stride + ch, val);
+                    else
+                        global_add(gr.grads + ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * C + ch,
+                                   val);
                 }
             }
         }
     }
-    __syncthreads();
-    // One task per (grid, 16-row tile of its cells), spread over the waves.
-    int task = 0;
+}
+
+// Part 2 (after the barrier): one task per (grid, 16-row tile of its cells), dealt to the
+// waves starting at wave `first`.
+template <class S, int C, int GM>
+__device__ __forceinline__ void scatter_reduce(const TrainDesc &d, const int (&cbx)[NT_MAX_GRIDS],
+                                               const int (&cby)[NT_MAX_GRIDS],
+                                               const int (&flo_x)[NT_MAX_GRIDS],
+                                               const int (&flo_y)[NT_MAX_GRIDS], float *fp,
+                                               const _Float16 *sct, int first, int wave, int lane)
+{
+    const _Float16 *dxt = sct;
+    const _Float16 *whi = dxt + S::K0 * kRowStride;
+    const _Float16 *wlo = whi + d.w_rows * kRowStride;
+    int task = first;
 #pragma unroll
-    for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
-        if (gi >= d.G)
-            break;
+    for (int gi = 0; gi < GM; ++gi) {
         const GridDesc &gr = d.grid[gi];
         const int ncell = gr.cb_w * gr.cb_h;
         const int ntile = (ncell + 15) >> 4;
@@ -605,36 +625,30 @@ __device__ __forceinline__ void scatter_mfma(const TrainDesc &d, const SampleFoo
             if ((task & 3) != wave)
                 continue;
             f4v acc = {0.f, 0.f, 0.f, 0.f};
-            const _Float16 *ah = whi + (gr.w_row0 + 16 * t + (lane & 15)) * kRowStride + 8 * (lane >> 4);
-            const _Float16 *al = wlo + (gr.w_row0 + 16 * t + (lane & 15)) * kRowStride + 8 * (lane >> 4);
+            const int arow = (gr.w_row0 + 16 * t + (lane & 15)) * kRowStride + 8 * (lane >> 4);
             const _Float16 *bp = dxt + (gi * C + (lane & 15)) * kRowStride + 8 * (lane >> 4);
 #pragma unroll
             for (int k = 0; k < kChunk / 32; ++k) {
-                const h8 b = *(const h8 *)(bp + 32 * k);
-                acc = mfma16(*(const h8 *)(ah + 32 * k), b, acc);
-                acc = mfma16(*(const h8 *)(al + 32 * k), b, acc);
+                const h8 bv = *(const h8 *)(bp + 32 * k);
+                acc = mfma16(*(const h8 *)(whi + arow + 32 * k), bv, acc);
+                acc = mfma16(*(const h8 *)(wlo + arow + 32 * k), bv, acc);
             }
             const int ch = lane & 15;
-            if (ch < C) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int cell = 16 * t + 4 * (lane >> 4) + r;
-                    if (cell >= ncell || acc[r] == 0.f)
-                        continue;
-                    const int tx = cbx0[gi] + cell % gr.cb_w, ty = cby0[gi] + cell / gr.cb_w;
-                    const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
-                    if (lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h) {
-                        float *p = fp + gr.fp_off + (ly * gr.fp_w + lx) * d.fp_stride + ch;
-                        *p += acc[r];
-                    } else {
-                        global_add(gr.grads + ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * C + ch,
-                                   acc[r]);
-                    }
-                }
+            for (int r = 0; r < 4; ++r) {
+                const int cell = 16 * t + 4 * (lane >> 4) + r;
+                if (cell >= ncell || acc[r] == 0.f)
+                    continue;
+                const int tx = cbx[gi] + cell % gr.cb_w, ty = cby[gi] + cell / gr.cb_w;
+                const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
+                if (lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h)
+                    fp[gr.fp_off + (ly * gr.fp_w + lx) * d.fp_stride + ch] += acc[r];
+                else
+                    global_add(gr.grads + ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * C + ch,
+                               acc[r]);
             }
         }
     }
-    __syncthreads();
 }
 
 // Backward through hidden layer l (its input is hidden activation l-1), then l-1 ... 1.
@@ -671,6 +685,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 {
     using LY = TrainLayout<S>;
     constexpr int L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
+    constexpr int GM = C == 16 ? S::K0 / 16 : NT_MAX_GRIDS; // grids, as far as known statically
     extern __shared__ __align__(16) unsigned char smem[];
     h8 *frags = (h8 *)smem;
     float *bias = (float *)(smem + LY::frag_bytes);
@@ -678,6 +693,9 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
     unsigned char *un = smem + d.union_off;
     _Float16 *xt = (_Float16 *)un;
     _Float16 *dyt = xt + LY::xt_rows * kRowStride;
+    float4 *tile = (float4 *)un; // aliases the transposes: dead before they are written
+    // Scatter matrices: their own region when it fits (scatter_split), else the union.
+    _Float16 *sct = (_Float16 *)(smem + (d.scatter_split ? d.scatter_off : d.union_off));
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
     {
@@ -689,7 +707,6 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
     }
     for (int i = tid; i < d.fp_floats; i += kTrainThreads)
         fp[i] = 0.f;
-    float4 *tile = (float4 *)un; // aliases the transposes: used before them in every chunk
 
     const int tile_x = blockIdx.x % d.tiles_x, tile_y = blockIdx.x / d.tiles_x;
     const int tx0 = tile_x * kChunkW * d.chunks_per_wg, ty0 = tile_y * kChunkH;
@@ -698,10 +715,9 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 #pragma unroll
     for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
         const GridDesc &gr = d.grid[gi];
-        flo_x[gi] = (int)floorf((float)(d.off_x + tx0) * (float)gr.w / (float)d.image_w - 0.5f) - 1;
-        flo_y[gi] = (int)floorf((float)(d.off_y + ty0) * (float)gr.h / (float)d.image_h - 0.5f) - 1;
+        flo_x[gi] = gi < GM ? (int)floorf((float)(d.off_x + tx0) * (float)gr.w / (float)d.image_w - 0.5f) - 1 : 0;
+        flo_y[gi] = gi < GM ? (int)floorf((float)(d.off_y + ty0) * (float)gr.h / (float)d.image_h - 0.5f) - 1 : 0;
     }
-    __syncthreads();
 
     f16v dwacc[LY::slots];
 #pragma unroll
@@ -714,13 +730,16 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
     for (int l = 0; l < L; ++l)
         dbacc[l] = 0.f;
 
+    const bool mfma_scatter = TYPE == NT_UNCONSTRAINED && C == 16 && d.scatter_mfma;
     const int col = 32 * wave + c; // column of this lane's sample in the LDS transposes
     for (int chunk = 0; chunk < d.chunks_per_wg; ++chunk) {
         const int cx0 = d.off_x + tx0 + chunk * kChunkW, cy0 = d.off_y + ty0;
-        if (d.tile_ok) {
+        if (mfma_scatter && d.scatter_split)
+            zero_scatter_weights(d, sct, tid, S::K0); // last read before the previous chunk's final barrier
+        if (d.tile_ok)
             load_target_tile(d, tile, cx0, cy0, tid);
-            __syncthreads();
-        }
+        __syncthreads(); // weights staged / footprint box zeroed / tile loaded
+
         // ---- sample position (train.cu:827-844)
         const int sx = tx0 + chunk * kChunkW + (c & 15);
         const int sy = ty0 + 2 * wave + (c >> 4);
@@ -736,25 +755,20 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
         const float u = px / (float)d.image_w;
         const float v = py / (float)d.image_h;
 
-        SampleFootprints fps;
-        sample_footprints(d, u, v, fps);
         h8 x0[KQ0];
-        if (valid) {
-            if constexpr (TYPE == NT_UNCONSTRAINED)
-                gather_unconstrained<C, KQ0>(d, fps, g, x0);
-            else
-                gather_bc6<C, KQ0>(d, fps, g, x0);
-        } else {
+        {
+            SampleFootprints fps;
+            sample_footprints<GM>(d, u, v, fps);
+            if (valid) {
+                if constexpr (TYPE == NT_UNCONSTRAINED)
+                    gather_unconstrained<C, KQ0>(d, fps, g, x0);
+                else
+                    gather_bc6<C, KQ0>(d, fps, g, x0);
+            } else {
 #pragma unroll
-            for (int q = 0; q < KQ0; ++q)
-                x0[q] = (h8)(_Float16)0.f;
-        }
-        float tgt[8], tw[8];
-        if (d.tile_ok) {
-            lane_targets_tile(d, tile, cx0, cy0, u, v, g, tgt, tw);
-            __syncthreads(); // the transposes below overwrite the tile
-        } else {
-            lane_targets(d, u, v, g, tgt, tw);
+                for (int q = 0; q < KQ0; ++q)
+                    x0[q] = (h8)(_Float16)0.f;
+            }
         }
 
         // ---- forward (mlp.h:65-99)
@@ -770,12 +784,17 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
                 to_fragments<HQ, HA, true>(acc, xh[l]);
             }
         }
-        // ---- loss gradient (train.cu:876-888): dL/dy = fp16(2 w (y - t) / N)
+        // ---- targets and loss gradient (train.cu:105-157, 876-888): dL/dy = fp16(2 w (y - t) / N)
         h8 dyo[1];
         {
             f16v out[1];
             layer_forward<HQ, 1>(frags + S::fwd_off(L - 1) * kWave, bias + S::bias_off(L - 1),
                                  xh[NH - 1], out, lane);
+            float tgt[8], tw[8];
+            if (d.tile_ok)
+                lane_targets_tile(d, tile, cx0, cy0, u, v, g, tgt, tw);
+            else
+                lane_targets(d, u, v, g, tgt, tw);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float y = (float)(_Float16)out[0][e];
@@ -784,6 +803,8 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
                 dyo[0][e] = valid ? (_Float16)gr : (_Float16)0.f;
             }
         }
+        if (d.tile_ok)
+            __syncthreads(); // the transposes below overwrite the tile
 
         // ---- backward, last layer (mlp.h:302-362)
         h8 dyh[HQ];
@@ -820,18 +841,36 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
                 for (int e = 0; e < 8; ++e)
                     dx0[q][e] = (_Float16)acc[q >> 1][8 * (q & 1) + e];
         }
+        // Footprints again (cheaper than keeping them live through the MLP).
+        SampleFootprints fps;
+        sample_footprints<GM>(d, rn32(u), rn32(v), fps);
+        int cbx[NT_MAX_GRIDS], cby[NT_MAX_GRIDS];
+        if constexpr (TYPE == NT_UNCONSTRAINED && C == 16) {
+            chunk_box<GM>(d, cx0, cy0, cbx, cby);
+            if (mfma_scatter && d.scatter_split)
+                scatter_write<S, C, GM>(d, fps, dx0, valid, cbx, cby, flo_x, flo_y, fp, sct, col, g);
+        }
         __syncthreads();
         dw_phase<S, 0>(xt, dyt, dwacc, dbacc[0], wave, lane, tid);
+        if constexpr (TYPE == NT_UNCONSTRAINED && C == 16) {
+            if (mfma_scatter && d.scatter_split)
+                scatter_reduce<S, C, GM>(d, cbx, cby, flo_x, flo_y, fp, sct, S::dw_total(), wave, lane);
+        }
         __syncthreads();
 
-        // ---- latent gradient scatter
+        // ---- latent gradient scatter when it cannot share the layer-0 phase
         if constexpr (TYPE == NT_UNCONSTRAINED) {
             if constexpr (C == 16) {
-                if (d.scatter_mfma)
-                    scatter_mfma<S, C>(d, fps, dx0, valid, cx0, cy0, flo_x, flo_y, fp, un, col, wave,
-                                       lane, tid);
-                else if (valid)
+                if (mfma_scatter && !d.scatter_split) {
+                    zero_scatter_weights(d, sct, tid, S::K0);
+                    __syncthreads();
+                    scatter_write<S, C, GM>(d, fps, dx0, valid, cbx, cby, flo_x, flo_y, fp, sct, col, g);
+                    __syncthreads();
+                    scatter_reduce<S, C, GM>(d, cbx, cby, flo_x, flo_y, fp, sct, 0, wave, lane);
+                    __syncthreads();
+                } else if (!mfma_scatter && valid) {
                     scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
+                }
             } else {
                 if (valid)
                     scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
@@ -851,7 +890,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
                 continue;
             int gi = 0;
 #pragma unroll
-            for (int k = 1; k < NT_MAX_GRIDS; ++k)
+            for (int k = 1; k < GM; ++k)
                 if (k < d.G && i >= d.grid[k].fp_off)
                     gi = k;
             const GridDesc &gr = d.grid[gi];
@@ -862,7 +901,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
             const int lx = cell % gr.fp_w, ly = cell / gr.fp_w;
             int lox = flo_x[0], loy = flo_y[0];
 #pragma unroll
-            for (int k = 1; k < NT_MAX_GRIDS; ++k)
+            for (int k = 1; k < GM; ++k)
                 if (gi == k) {
                     lox = flo_x[k];
                     loy = flo_y[k];
