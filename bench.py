@@ -34,6 +34,10 @@ PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 FLOP_PER_TRAIN_SAMPLE_C2 = 40320   # 3 x 2 x (32*64 + 64*64 + 64*9)
 FLOP_PER_DECODE_PIXEL = 26112      # 2 x (64*64*3 + 64*12)
+# HBM bytes per config-2 train-kernel launch: rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000,
+# the factors being what the two counters read for a 256 MiB device copy (--copy-probe).
+# Counters cannot be read live; re-measure whenever the train kernel changes.
+TRAIN_HBM_BYTES_PER_LAUNCH = (9075.4 * 2.0 + 18664.0) * 1024
 
 
 def log(msg):
@@ -327,7 +331,8 @@ def main():
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_FP16_TFLOPS,
-            "traffic": None,
+            "traffic": TRAIN_HBM_BYTES_PER_LAUNCH,
+            "traffic_unit": "bytes/launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
             "launch_ms_mean": kernel_ms,
             "launch_ms_median": kernel_med,
             "flop_per_launch": kflops,

@@ -15,6 +15,16 @@
  *   - MLP dot products accumulate in double here (the GPU accumulates in fp32 MFMA);
  *     results are compared with a tolerance, as the reference itself is order-
  *     nondeterministic (float atomics).
+ *
+ * Parity unpinned: the reference's MLP runs inside tiny-cuda-nn (mlp.h:7), which is not
+ * in the reference tree (absent submodule, unknown commit). Its internal numerics
+ * (accumulator precision, fp16 per-warp weight-gradient partials mlp.h:170-172,
+ * activate_bwd at exactly 0) are not reproduced. ntref_mlp_forward_one beyond the 2-layer
+ * known answers of tests/forward_pass_test.cu, and ntref_mlp_backward_one, are pinned by
+ * mathematics only (float64 GEMM, finite differences), not by reference outputs.
+ * Reference-texture sampling uses the exact 16-tap Catmull-Rom; the reference's 9 hardware
+ * bilinear fetches with 8-bit fractional weights (filter/catmull_rom.h:76-86) are not
+ * emulated.
  */
 #ifndef NT_ORACLE_H
 #define NT_ORACLE_H
