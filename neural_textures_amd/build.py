@@ -20,6 +20,9 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libnt_hip.so")
 SOURCES = ["nt_api.cpp", "nt_train.hip", "nt_forward.hip", "nt_adam.hip", "nt_codec.hip"]
+HOST_DIR = os.path.join(HERE, "host")
+HOST_SOURCES = ["nt_host.cpp", "nt_train_main.cpp"]
+HOST_PROGRAM = os.path.join(HOST_DIR, "nt_train")
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -61,9 +64,31 @@ def build(verbose: bool = False) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIBRARY)
+    build_host()
     if verbose:
-        print(f"built {LIBRARY}")
+        print(f"built {LIBRARY} and {HOST_PROGRAM}")
     return LIBRARY
+
+
+def build_host() -> str:
+    """Builds the C++ host program (host/nt_train) against libnt_hip.so."""
+    objs = []
+    for src in HOST_SOURCES:
+        obj = os.path.join(BUILD_DIR, "host_" + os.path.splitext(src)[0] + ".o")
+        cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", os.path.join(HOST_DIR, src),
+               "-o", obj]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed for host/{src}:\n{res.stdout}\n{res.stderr}")
+        objs.append(obj)
+    tmp = HOST_PROGRAM + ".tmp"
+    cmd = [HIPCC, "-o", tmp, *objs, "-L" + HERE, "-lnt_hip", "-Wl,-rpath,$ORIGIN/..",
+           "-Wl,-rpath,/opt/rocm/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, HOST_PROGRAM)
+    return HOST_PROGRAM
 
 
 if __name__ == "__main__":

@@ -1,0 +1,400 @@
+// nt_host.cpp — host-side storage, initialisation, session and training loop over the C ABI.
+#include "nt_host.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+
+namespace nt_host {
+
+const ModeConfig kModes[4] = {
+    // main.cpp:72-77
+    {"BCf-0.5k", {{{512, 8}, {256, 7}, {128, 6}, {64, 5}}}},
+    {"BCf-1k", {{{1024, 9}, {512, 8}, {256, 7}, {128, 6}}}},
+    {"BCf-2k", {{{2048, 10}, {1024, 9}, {512, 8}, {256, 7}}}},
+    {"BCf-2k++", {{{2048, 10}, {2048, 10}, {512, 8}, {256, 7}}}},
+};
+
+void check(int status, const char *what)
+{
+    if (status != NT_OK)
+        throw Error(std::string(what) + ": " + nt_status_string(status) + " (" + nt_last_error() + ")");
+}
+
+void check_hip(hipError_t err, const char *what)
+{
+    if (err != hipSuccess)
+        throw Error(std::string(what) + ": " + hipGetErrorString(err));
+}
+
+uint16_t float_to_half(float f)
+{
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    x &= 0x7fffffffu;
+    if (x >= 0x7f800000u) // inf / nan
+        return (uint16_t)(sign | 0x7c00u | (x > 0x7f800000u ? 0x200u : 0u));
+    if (x >= 0x477ff000u) // rounds to >= 65520: overflow to inf
+        return (uint16_t)(sign | 0x7c00u);
+    if (x < 0x38800000u) { // below the smallest normal half: subnormal or zero
+        if (x < 0x33000000u)
+            return (uint16_t)sign; // < 2^-25 rounds to zero
+        const uint32_t mant = (x & 0x7fffffu) | 0x800000u;
+        const int shift = 126 - (int)(x >> 23); // 14 + (113 - exp)
+        uint32_t v = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (v & 1u)))
+            ++v;
+        return (uint16_t)(sign | v);
+    }
+    uint32_t v = ((x - 0x38000000u) >> 13); // rebias exponent 127 -> 15
+    const uint32_t rem = x & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (v & 1u)))
+        ++v;
+    return (uint16_t)(sign | v);
+}
+
+float half_to_float(uint16_t h)
+{
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    float f;
+    if (e == 0)
+        f = std::ldexp((float)m, -24);
+    else if (e == 31)
+        f = m ? NAN : INFINITY;
+    else
+        f = std::ldexp((float)(m | 0x400u), (int)e - 25);
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    x |= sign;
+    std::memcpy(&f, &x, 4);
+    return f;
+}
+
+// ---- latent grids ------------------------------------------------------------------
+
+void LatentGrid::allocate(int w, int h, int mips, int c, bool with_blocks)
+{
+    if (mips < 1 || mips > NT_MAX_MIPS)
+        throw Error("bad mip count");
+    width = w, height = h, num_mips = mips, channels = c;
+    texels = nt_mip_chain_layout(w, h, mips, mip_offset);
+    blocks = nt_block_chain_layout(w, h, mips, block_offset);
+    if (texels < 0 || blocks < 0)
+        throw Error("bad grid size");
+    const size_t n = (size_t)texels * (size_t)c;
+    values.allocate(n);
+    grads.allocate(n);
+    moment1.allocate(n);
+    moment2.allocate(n);
+    grads.zero();
+    moment1.zero();
+    moment2.zero();
+    if (with_blocks) {
+        const size_t rec = 4 * (size_t)c + 16;
+        block_params.allocate((size_t)blocks * (rec + 2));
+        block_grads.allocate((size_t)blocks * rec);
+        block_moment1.allocate((size_t)blocks * rec);
+        block_moment2.allocate((size_t)blocks * rec);
+        block_params.zero(); // main.cpp:686-692: the block storage starts zeroed
+        block_grads.zero();
+        block_moment1.zero();
+        block_moment2.zero();
+    }
+}
+
+void LatentGrid::initialize(std::mt19937 &rng)
+{
+    std::uniform_real_distribution<float> dist(0.f, 1.f);
+    std::vector<float> h((size_t)texels * (size_t)channels);
+    for (float &v : h)
+        v = dist(rng);
+    values.upload(h);
+}
+
+nt_grid LatentGrid::view() const
+{
+    nt_grid g{};
+    g.width = width, g.height = height, g.num_mips = num_mips;
+    for (int m = 0; m < num_mips; ++m) {
+        g.mip_offset[m] = mip_offset[m];
+        g.block_offset[m] = block_offset[m];
+    }
+    g.values = values.get();
+    g.grads = grads.get();
+    g.moment1 = moment1.get();
+    g.moment2 = moment2.get();
+    g.block_params = block_params.get();
+    g.block_grads = block_grads.get();
+    g.block_moment1 = block_moment1.get();
+    g.block_moment2 = block_moment2.get();
+    return g;
+}
+
+// ---- network -------------------------------------------------------------------------
+
+static int pad16(int x) { return (x + 15) & ~15; }
+
+void Network::allocate(const std::vector<int> &s, int used)
+{
+    if (s.size() < 3 || s.size() > NT_MAX_LAYERS + 1)
+        throw Error("network needs 2..6 layers");
+    sizes = s;
+    used_outputs = std::clamp(used, 0, s.back());
+    const int L = (int)s.size() - 1;
+    weights.resize(L), biases.resize(L);
+    weight_grads.resize(L), weight_m1.resize(L), weight_m2.resize(L);
+    bias_grads.resize(L), bias_m1.resize(L), bias_m2.resize(L);
+    for (int l = 0; l < L; ++l) {
+        const size_t nw = (size_t)pad16(s[l]) * pad16(s[l + 1]), nb = (size_t)s[l + 1];
+        weights[l].allocate(nw);
+        weight_grads[l].allocate(nw);
+        weight_m1[l].allocate(nw);
+        weight_m2[l].allocate(nw);
+        biases[l].allocate(nb);
+        bias_grads[l].allocate(nb);
+        bias_m1[l].allocate(nb);
+        bias_m2[l].allocate(nb);
+        for (auto *a : {&weight_grads[l], &weight_m1[l], &weight_m2[l], &bias_grads[l], &bias_m1[l], &bias_m2[l]})
+            a->zero();
+        weights[l].zero();
+        biases[l].zero();
+    }
+}
+
+void Network::initialize(std::mt19937 &rng, float scale)
+{
+    const int L = (int)sizes.size() - 1;
+    for (int l = 0; l < L; ++l) {
+        std::uniform_real_distribution<float> dist(-scale, scale);
+        const int rows = pad16(sizes[l]);
+        const int active_rows = sizes[l];
+        const int active_cols = l == L - 1 ? used_outputs : sizes[l + 1];
+        std::vector<uint16_t> w((size_t)rows * pad16(sizes[l + 1]), 0);
+        for (int col = 0; col < active_cols; ++col)
+            for (int row = 0; row < active_rows; ++row)
+                w[(size_t)col * rows + row] = float_to_half(dist(rng));
+        weights[l].upload(w);
+    }
+}
+
+nt_mlp Network::view() const
+{
+    nt_mlp m{};
+    m.num_layers = (int)sizes.size() - 1;
+    for (size_t i = 0; i < sizes.size(); ++i)
+        m.sizes[i] = sizes[i];
+    m.used_outputs = used_outputs;
+    for (int l = 0; l < m.num_layers; ++l) {
+        m.weights[l] = weights[l].get();
+        m.weight_grads[l] = weight_grads[l].get();
+        m.weight_moment1[l] = weight_m1[l].get();
+        m.weight_moment2[l] = weight_m2[l].get();
+        m.biases[l] = biases[l].get();
+        m.bias_grads[l] = bias_grads[l].get();
+        m.bias_moment1[l] = bias_m1[l].get();
+        m.bias_moment2[l] = bias_m2[l].get();
+    }
+    return m;
+}
+
+// ---- textures ------------------------------------------------------------------------
+
+nt_texture Texture::view() const
+{
+    nt_texture t{};
+    t.texels = texels.get();
+    t.width = width, t.height = height, t.num_channels = channels;
+    t.num_mips = 1;
+    t.pitch = pitch;
+    t.loss_weight = loss_weight;
+    return t;
+}
+
+Texture upload_texture(int width, int height, int channels, const std::vector<float> &pixels,
+                       float loss_weight)
+{
+    if (channels < 1 || (size_t)width * height * channels != pixels.size())
+        throw Error("texture size mismatch");
+    Texture t;
+    t.width = width, t.height = height, t.channels = channels;
+    t.pitch = channels == 1 ? 1 : 4;
+    t.loss_weight = loss_weight;
+    const int used = std::min(channels, t.pitch);
+    std::vector<float> h((size_t)width * height * t.pitch, 0.f);
+    for (size_t p = 0; p < (size_t)width * height; ++p)
+        for (int c = 0; c < used; ++c)
+            h[p * t.pitch + c] = pixels[p * channels + c];
+    t.texels.allocate(h.size());
+    t.texels.upload(h);
+    return t;
+}
+
+std::vector<float> synthetic_channel(int width, int height, uint32_t seed, int cell)
+{
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<float> u(-1.f, 1.f);
+    const int gw = width / cell + 2, gh = height / cell + 2;
+    std::vector<float> lattice((size_t)gw * gh);
+    for (float &v : lattice)
+        v = u(rng);
+    std::uniform_int_distribution<int> freq(1, 8);
+    const int fx = freq(rng), fy = freq(rng);
+    const float phi = std::uniform_real_distribution<float>(0.f, 6.2831853f)(rng);
+    std::vector<float> out((size_t)width * height);
+    for (int y = 0; y < height; ++y) {
+        const float ty = (float)y / cell;
+        const int y0 = (int)ty;
+        float fyv = ty - y0;
+        fyv = fyv * fyv * (3.f - 2.f * fyv);
+        for (int x = 0; x < width; ++x) {
+            const float tx = (float)x / cell;
+            const int x0 = (int)tx;
+            float fxv = tx - x0;
+            fxv = fxv * fxv * (3.f - 2.f * fxv);
+            const float *r0 = &lattice[(size_t)y0 * gw], *r1 = r0 + gw;
+            const float noise = (r0[x0] * (1 - fxv) + r0[x0 + 1] * fxv) * (1 - fyv) +
+                                (r1[x0] * (1 - fxv) + r1[x0 + 1] * fxv) * fyv;
+            const float wave =
+                std::sin(6.2831853f * (fx * (float)x / width + fy * (float)y / height) + phi);
+            out[(size_t)y * width + x] = std::clamp(0.5f + 0.25f * noise + 0.25f * wave, 0.f, 1.f);
+        }
+    }
+    return out;
+}
+
+int packed_channel_count(const std::vector<Texture> &textures)
+{
+    int n = 0;
+    for (const Texture &t : textures) {
+        n += t.channels == 1 ? 1 : std::min(t.channels, 4);
+        if (n >= NT_MAX_OUTPUTS)
+            return NT_MAX_OUTPUTS;
+    }
+    return n;
+}
+
+// ---- session -------------------------------------------------------------------------
+
+Session::Session(const SessionConfig &cfg, std::vector<Texture> tex, hipStream_t stream)
+    : textures(std::move(tex)), stream_(stream)
+{
+    if (cfg.mode < 0 || cfg.mode > 3)
+        throw Error("mode must be 0..3");
+    if (cfg.num_grids < 1 || cfg.num_grids > NT_MAX_GRIDS)
+        throw Error("num_grids must be 1..4");
+    if (textures.empty() || (int)textures.size() > NT_MAX_TEXTURES)
+        throw Error("1..16 reference textures needed");
+    // InitializeTrainingMode, main.cpp:796-826: one generator for grids then network.
+    std::mt19937 rng(cfg.seed_base + (uint32_t)cfg.mode);
+    const ModeConfig &mode = kModes[cfg.mode];
+    grids.resize(cfg.num_grids);
+    for (int g = 0; g < cfg.num_grids; ++g) {
+        grids[g].allocate(mode.grids[g].resolution, mode.grids[g].resolution, mode.grids[g].num_mips,
+                          cfg.channels, cfg.with_blocks);
+        grids[g].initialize(rng);
+    }
+    std::vector<int> sizes;
+    sizes.push_back(cfg.num_grids * cfg.channels);
+    for (int h : cfg.hidden)
+        sizes.push_back(h);
+    sizes.push_back(NT_MAX_OUTPUTS);
+    network.allocate(sizes, packed_channel_count(textures));
+    network.initialize(rng, cfg.init_scale);
+
+    params_.feature_adam = nt_adam{0.9f, 0.999f, cfg.feature_lr, 1e-8f};
+    params_.network_adam = nt_adam{0.9f, 0.999f, cfg.network_lr, 1e-8f};
+    // The sampling domain is the reference textures' size, all equal (main.cpp:965-979).
+    params_.image_width = textures[0].width;
+    params_.image_height = textures[0].height;
+    for (const Texture &t : textures)
+        if (t.width != params_.image_width || t.height != params_.image_height)
+            throw Error("all reference textures must have the same dimensions");
+    params_.num_samples = 512 * 512; // main.cpp:825
+    params_.region_width = 512;
+    params_.step = 0;
+    refresh_views();
+
+    const size_t pixels = (size_t)params_.image_width * params_.image_height;
+    inference_out_.allocate(pixels * (size_t)NT_MAX_OUTPUTS);
+    mse_accum_.allocate(1);
+    params_.inference_output = inference_out_.get();
+    params_.inference_mse_accum = mse_accum_.get();
+
+    const size_t ws = std::max(nt_train_workspace_bytes(&params_, NT_UNCONSTRAINED),
+                               cfg.with_blocks ? nt_train_workspace_bytes(&params_, NT_BLOCK_FEATURES) : 0);
+    if (ws == 0)
+        check(NT_ERR_INVALID_ARGUMENT, "nt_train_workspace_bytes");
+    workspace_.allocate(ws);
+    params_.workspace = workspace_.get();
+    params_.workspace_bytes = ws;
+}
+
+void Session::refresh_views()
+{
+    params_.latents.num_grids = (int)grids.size();
+    params_.latents.channels = grids.empty() ? 0 : grids[0].channels;
+    for (size_t g = 0; g < grids.size(); ++g)
+        params_.latents.grids[g] = grids[g].view();
+    params_.mlp = network.view();
+    params_.num_textures = (int)textures.size();
+    for (size_t t = 0; t < textures.size(); ++t)
+        params_.textures[t] = textures[t].view();
+}
+
+void Session::train(nt_kernel_type type) { check(nt_train_step(&params_, type, stream_), "nt_train_step"); }
+
+void Session::optimize_network() { check(nt_optimize_network(&params_, stream_), "nt_optimize_network"); }
+
+void Session::optimize_features(nt_kernel_type type)
+{
+    check(nt_optimize_latents(&params_, type, stream_), "nt_optimize_latents");
+}
+
+void Session::synchronize() { check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize"); }
+
+double Session::inference_mse()
+{
+    check_hip(hipMemsetAsync(mse_accum_.get(), 0, sizeof(float), stream_), "hipMemsetAsync");
+    check(nt_inference(&params_, stream_), "nt_inference");
+    synchronize();
+    float sse = 0.f;
+    check_hip(hipMemcpy(&sse, mse_accum_.get(), sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+    const double pixels = (double)params_.image_width * params_.image_height;
+    return (double)sse / (pixels * std::max(1, packed_channel_count(textures)));
+}
+
+double run_training_loop(Session &s, const LoopOptions &opt)
+{
+    nt_params &p = s.params();
+    const int max_x = std::max(0, p.image_width - opt.region);
+    const int max_y = std::max(0, p.image_height - opt.region);
+    const float base_lr = p.feature_adam.learning_rate;
+    std::mt19937 region_rng(opt.region_seed);
+    std::uniform_int_distribution<int> rx(0, max_x), ry(0, max_y);
+    const auto start = std::chrono::steady_clock::now();
+    double elapsed = 0.0;
+    for (int iter = 0; iter < opt.max_iters; ++iter) {
+        p.texel_offset_x = rx(region_rng);
+        p.texel_offset_y = ry(region_rng);
+        p.feature_adam.learning_rate = base_lr * std::pow(opt.feature_gamma, (float)iter);
+        s.train(opt.type);
+        s.optimize_network();
+        if (opt.type != NT_FINALIZE)
+            s.optimize_features(opt.type);
+        p.step++;
+        if ((iter + 1) % opt.progress_interval == 0 || iter + 1 == opt.max_iters) {
+            s.synchronize();
+            elapsed = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+            if (opt.log)
+                std::fprintf(opt.log, "Completed iteration %d / %d (%.2fs)\n", iter + 1, opt.max_iters, elapsed);
+        }
+    }
+    p.feature_adam.learning_rate = base_lr;
+    return elapsed;
+}
+
+} // namespace nt_host

@@ -1,0 +1,215 @@
+// nt_host.hpp — C++ host side of the train/decode path, over the C ABI of include/nt/nt.h.
+//
+// Mirrors the reference host program (mavenkim2/neural_textures main.cpp) for the hot path:
+// latent-grid and network storage with the reference's initialisation order
+// (main.cpp:182-214, 657-826), a KernelParams-like session whose methods stand where the
+// reference calls InvokeTraining / InvokeOptimizeNetwork / InvokeOptimizeFeatures /
+// InvokeInference (train.h:158-161), and the training loop of main.cpp:1017-1109.
+// Device memory is owned here (hipMalloc), as the reference host owns it
+// (AllocateDeviceBuffer, main.cpp:147-153); the library itself never allocates.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <array>
+#include <cstdint>
+#include <cstdio>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/nt/nt.h"
+
+namespace nt_host {
+
+// A failing library or HIP call (the reference's CheckCuda, main.cpp:103-110).
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+void check(int status, const char *what);
+void check_hip(hipError_t err, const char *what);
+
+// Owning device array.
+template <class T> class DeviceArray {
+  public:
+    DeviceArray() = default;
+    explicit DeviceArray(size_t n) { allocate(n); }
+    DeviceArray(const DeviceArray &) = delete;
+    DeviceArray &operator=(const DeviceArray &) = delete;
+    DeviceArray(DeviceArray &&o) noexcept : ptr_(o.ptr_), n_(o.n_) { o.ptr_ = nullptr, o.n_ = 0; }
+    DeviceArray &operator=(DeviceArray &&o) noexcept
+    {
+        if (this != &o) {
+            release();
+            ptr_ = o.ptr_, n_ = o.n_;
+            o.ptr_ = nullptr, o.n_ = 0;
+        }
+        return *this;
+    }
+    ~DeviceArray() { release(); }
+
+    void allocate(size_t n)
+    {
+        release();
+        if (n) {
+            check_hip(hipMalloc(reinterpret_cast<void **>(&ptr_), n * sizeof(T)), "hipMalloc");
+            n_ = n;
+        }
+    }
+    void zero()
+    {
+        if (n_)
+            check_hip(hipMemset(ptr_, 0, n_ * sizeof(T)), "hipMemset");
+    }
+    void upload(const std::vector<T> &h)
+    {
+        if (h.size() != n_)
+            throw Error("upload size mismatch");
+        if (n_)
+            check_hip(hipMemcpy(ptr_, h.data(), n_ * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D");
+    }
+    std::vector<T> download() const
+    {
+        std::vector<T> h(n_);
+        if (n_)
+            check_hip(hipMemcpy(h.data(), ptr_, n_ * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+        return h;
+    }
+    T *get() const { return ptr_; }
+    size_t size() const { return n_; }
+
+  private:
+    void release()
+    {
+        if (ptr_)
+            (void)hipFree(ptr_);
+        ptr_ = nullptr, n_ = 0;
+    }
+    T *ptr_ = nullptr;
+    size_t n_ = 0;
+};
+
+// Latent pyramid of one training mode (FeatureModeConfig / TrainingModeConfig,
+// main.cpp:60-77).
+struct GridConfig {
+    int resolution;
+    int num_mips;
+};
+struct ModeConfig {
+    const char *name;
+    std::array<GridConfig, 4> grids;
+};
+extern const ModeConfig kModes[4];
+
+// IEEE binary16 round-to-nearest-even (what __float2half does).
+uint16_t float_to_half(float f);
+float half_to_float(uint16_t h);
+
+// One latent grid (Feature, train.h:51-67): unconstrained texels and BC6 block records
+// for the whole mip chain.
+class LatentGrid {
+  public:
+    void allocate(int width, int height, int num_mips, int channels, bool with_blocks);
+    // U[0, 1) per channel, texel by texel, mip by mip (InitializeFloat3Texels,
+    // main.cpp:201-214; with channels = 3 the draw order is the reference's).
+    void initialize(std::mt19937 &rng);
+    nt_grid view() const;
+
+    int width = 0, height = 0, num_mips = 0, channels = 0;
+    int64_t texels = 0, blocks = 0;
+    int64_t mip_offset[NT_MAX_MIPS] = {};
+    int64_t block_offset[NT_MAX_MIPS] = {};
+    DeviceArray<float> values, grads, moment1, moment2;
+    DeviceArray<float> block_params, block_grads, block_moment1, block_moment2;
+};
+
+// The MLP (mlp.h) with its fp32 gradient and Adam state.
+class Network {
+  public:
+    void allocate(const std::vector<int> &sizes, int used_outputs);
+    // Column-outer, row-inner U[-scale, scale] draws over the active rows x cols of every
+    // layer, fp16 by round-to-nearest; biases and padding zero (InitializeNetworkWeightMatrix
+    // / InitializeNetworkStorage, main.cpp:182-199, 745-799).
+    void initialize(std::mt19937 &rng, float scale);
+    nt_mlp view() const;
+
+    std::vector<int> sizes;
+    int used_outputs = 0;
+    std::vector<DeviceArray<uint16_t>> weights, biases;
+    std::vector<DeviceArray<float>> weight_grads, weight_m1, weight_m2;
+    std::vector<DeviceArray<float>> bias_grads, bias_m1, bias_m2;
+};
+
+// A reference texture in device memory, mip 0, pitch 4 (or 1 for one channel).
+struct Texture {
+    int width = 0, height = 0, channels = 0, pitch = 4;
+    float loss_weight = 1.f;
+    DeviceArray<float> texels;
+    nt_texture view() const;
+};
+// Host pixels [y][x][channels] -> a device texture.
+Texture upload_texture(int width, int height, int channels, const std::vector<float> &pixels,
+                       float loss_weight = 1.f);
+// Seeded synthetic target channel in [0, 1]: value noise (lattice every `cell` pixels,
+// smoothstep) plus a sinusoid, both drawn from `seed`.
+std::vector<float> synthetic_channel(int width, int height, uint32_t seed, int cell = 32);
+// Packed channel count of a texture set (GetPackedChannelCount; train.cu:105-157 rules).
+int packed_channel_count(const std::vector<Texture> &textures);
+
+struct SessionConfig {
+    int mode = 0;                  // index into kModes
+    int num_grids = 4;             // the first num_grids grids of the mode
+    int channels = 3;              // per grid
+    std::vector<int> hidden = {32, 32};
+    float init_scale = 1e-2f;      // main.cpp:766
+    float feature_lr = 5e-2f;      // main.cpp:803
+    float network_lr = 1e-3f;      // main.cpp:808
+    bool with_blocks = false;      // allocate BC6 block storage
+    uint32_t seed_base = 1337u;    // mt19937(1337 + mode), main.cpp:798
+};
+
+// KernelParams plus the buffers it points at, and the four launchers.
+class Session {
+  public:
+    Session(const SessionConfig &cfg, std::vector<Texture> textures, hipStream_t stream = nullptr);
+
+    void train(nt_kernel_type type);              // InvokeTraining
+    void optimize_network();                      // InvokeOptimizeNetwork
+    void optimize_features(nt_kernel_type type);  // InvokeOptimizeFeatures
+    // InvokeInference + the MSE of main.cpp:1090-1109 (SSE / (pixels * packed channels)).
+    double inference_mse();
+
+    nt_params &params() { return params_; }
+    hipStream_t stream() const { return stream_; }
+    void synchronize();
+
+    std::vector<LatentGrid> grids;
+    Network network;
+    std::vector<Texture> textures;
+
+  private:
+    void refresh_views();
+    nt_params params_{};
+    hipStream_t stream_ = nullptr;
+    DeviceArray<unsigned char> workspace_;
+    DeviceArray<float> inference_out_, mse_accum_;
+};
+
+struct LoopOptions {
+    int max_iters = 1000;
+    int progress_interval = 1000;
+    int region = 512;                 // kTrainingRegionSize, main.cpp:1023
+    float feature_gamma = 0.9995f;    // kUnconstrainedFeatureGamma, main.cpp:1027
+    uint32_t region_seed = 20260411u; // main.cpp:1033
+    nt_kernel_type type = NT_UNCONSTRAINED;
+    FILE *log = stdout;
+};
+
+// The training loop of main.cpp:1017-1087: per iteration a random region origin, the
+// feature learning-rate decay, train -> optimize network -> optimize features -> step++,
+// and a progress line with elapsed seconds every progress_interval iterations.
+// Returns the elapsed seconds.
+double run_training_loop(Session &s, const LoopOptions &opt);
+
+} // namespace nt_host

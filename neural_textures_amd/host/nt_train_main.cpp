@@ -1,0 +1,160 @@
+// nt_train — the reference program's training run (main.cpp:927-1109) on synthetic
+// targets: set up a training mode, train for N iterations with the reference schedule,
+// then run full-image inference and print its MSE.
+//
+//   nt_train [--mode M] [--grids G] [--channels C] [--hidden H,H,...] [--image S]
+//            [--targets T] [--iters N] [--progress K] [--feature-lr F] [--network-lr F]
+//            [--samples N] [--seed S] [--self-test]
+//
+// --self-test runs the host-only checks (no GPU) and exits.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <sstream>
+
+#include "nt_host.hpp"
+
+using namespace nt_host;
+
+namespace {
+
+int self_test()
+{
+    // fp16 conversion: exact on every finite half, round-to-nearest-even between them.
+    int bad = 0;
+    for (uint32_t h = 0; h < 0x10000u; ++h) {
+        const uint16_t hh = (uint16_t)h;
+        if ((hh & 0x7c00u) == 0x7c00u && (hh & 0x3ffu))
+            continue; // NaN
+        const float f = half_to_float(hh);
+        if (float_to_half(f) != hh)
+            ++bad;
+        if ((hh & 0x7fffu) < 0x7bffu) { // midpoint to the next half up (same sign)
+            const float g = half_to_float((uint16_t)(hh + 1));
+            const float mid = (float)(((double)f + (double)g) * 0.5);
+            const uint16_t want = (hh & 1u) ? (uint16_t)(hh + 1) : hh;
+            if (float_to_half(mid) != want)
+                ++bad;
+        }
+    }
+    if (float_to_half(65520.f) != 0x7c00u || float_to_half(65519.f) != 0x7bffu)
+        ++bad;
+    if (float_to_half(std::ldexp(1.f, -25)) != 0 || float_to_half(std::ldexp(1.1f, -25)) != 1)
+        ++bad;
+    // Mode table and layouts.
+    int64_t off[NT_MAX_MIPS];
+    if (nt_mip_chain_layout(kModes[0].grids[0].resolution, kModes[0].grids[0].resolution,
+                            kModes[0].grids[0].num_mips, off) != 349520) // 512^2 + 256^2 + ... + 4^2
+        ++bad;
+    if (kModes[2].grids[0].resolution != 2048 || kModes[2].grids[0].num_mips != 10)
+        ++bad;
+    // Synthetic target range.
+    const std::vector<float> t = synthetic_channel(64, 48, 7u);
+    for (float v : t)
+        if (!(v >= 0.f && v <= 1.f))
+            ++bad;
+    std::printf("self-test: %s (%d failures)\n", bad ? "FAILED" : "ok", bad);
+    return bad ? 1 : 0;
+}
+
+std::vector<int> parse_list(const char *s)
+{
+    std::vector<int> out;
+    std::stringstream ss(s);
+    std::string item;
+    while (std::getline(ss, item, ','))
+        out.push_back(std::atoi(item.c_str()));
+    return out;
+}
+
+} // namespace
+
+int main(int argc, char **argv)
+{
+    SessionConfig cfg;
+    LoopOptions loop;
+    int image = 2048, targets = 3, samples = 512 * 512;
+    uint32_t target_seed = 1u;
+    loop.max_iters = 1000;
+    for (int i = 1; i < argc; ++i) {
+        const char *a = argv[i];
+        auto next = [&]() -> const char * {
+            if (i + 1 >= argc) {
+                std::fprintf(stderr, "missing value for %s\n", a);
+                std::exit(2);
+            }
+            return argv[++i];
+        };
+        if (!std::strcmp(a, "--self-test"))
+            return self_test();
+        else if (!std::strcmp(a, "--mode"))
+            cfg.mode = std::atoi(next());
+        else if (!std::strcmp(a, "--grids"))
+            cfg.num_grids = std::atoi(next());
+        else if (!std::strcmp(a, "--channels"))
+            cfg.channels = std::atoi(next());
+        else if (!std::strcmp(a, "--hidden"))
+            cfg.hidden = parse_list(next());
+        else if (!std::strcmp(a, "--image"))
+            image = std::atoi(next());
+        else if (!std::strcmp(a, "--targets"))
+            targets = std::atoi(next());
+        else if (!std::strcmp(a, "--iters"))
+            loop.max_iters = std::atoi(next());
+        else if (!std::strcmp(a, "--progress"))
+            loop.progress_interval = std::atoi(next());
+        else if (!std::strcmp(a, "--feature-lr"))
+            cfg.feature_lr = (float)std::atof(next());
+        else if (!std::strcmp(a, "--network-lr"))
+            cfg.network_lr = (float)std::atof(next());
+        else if (!std::strcmp(a, "--samples"))
+            samples = std::atoi(next());
+        else if (!std::strcmp(a, "--seed"))
+            target_seed = (uint32_t)std::strtoul(next(), nullptr, 10);
+        else {
+            std::fprintf(stderr, "unknown option %s\n", a);
+            return 2;
+        }
+    }
+    if (loop.progress_interval < 1 || loop.max_iters < 0 || targets < 1 || targets > NT_MAX_OUTPUTS) {
+        std::fprintf(stderr, "bad arguments\n");
+        return 2;
+    }
+    try {
+        // Targets: `targets` channels packed 3 per texture (like RGB EXRs).
+        std::vector<Texture> tex;
+        for (int c = 0; c < targets; c += 3) {
+            const int n = std::min(3, targets - c);
+            std::vector<float> px((size_t)image * image * n);
+            for (int k = 0; k < n; ++k) {
+                const std::vector<float> ch = synthetic_channel(image, image, target_seed * 1000u + c + k);
+                for (size_t p = 0; p < ch.size(); ++p)
+                    px[p * n + k] = ch[p];
+            }
+            tex.push_back(upload_texture(image, image, n, px));
+        }
+        Session s(cfg, std::move(tex));
+        s.params().num_samples = samples;
+        const ModeConfig &mode = kModes[cfg.mode];
+        std::printf("Mode %d (%s)\n", cfg.mode, mode.name);
+        for (int g = 0; g < cfg.num_grids; ++g)
+            std::printf("  T%d: res=%d mips=%d channels=%d\n", g, s.grids[g].width, s.grids[g].num_mips,
+                        cfg.channels);
+        std::printf("Network:");
+        for (int n : s.network.sizes)
+            std::printf(" %d", n);
+        std::printf(" (used outputs %d)\n", s.network.used_outputs);
+        std::printf("Initial inference MSE: %.8f\n", s.inference_mse());
+        std::printf("Starting training for %d iterations\n", loop.max_iters);
+        const double secs = run_training_loop(s, loop);
+        const double mse = s.inference_mse();
+        std::printf("Train throughput: %.1f samples/s\n",
+                    secs > 0 ? (double)samples * loop.max_iters / secs : 0.0);
+        std::printf("Inference MSE: %.8f\n", mse);
+    } catch (const std::exception &e) {
+        std::fprintf(stderr, "nt_train: %s\n", e.what());
+        return 1;
+    }
+    return 0;
+}

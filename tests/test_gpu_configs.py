@@ -1,0 +1,143 @@
+"""GPU runs at the benchmark configurations' own shapes, checked against the CPU oracle.
+
+* Config 1: one 256x256x8 latent grid U[-1,1], Catmull-Rom sample at 65,536 uniform UVs,
+  MLP 8->64->64->3 (Xavier fp16): sampled features bit-exact, outputs within 1e-2 relative.
+* Loss-curve tracking: the full training loop (train step -> network Adam -> latent Adam
+  -> step++, feature lr decay 0.9995^i, a new region each step; main.cpp:1036-1077) runs
+  1,000 steps on the GPU and on the oracle from the same seeded state. Every 200 steps the
+  full-image inference MSE (train.cu:917-961) of the two must agree within 10 % relative:
+  both trajectories are order-nondeterministic at the 1e-3 level per step (fp16 MLP, float
+  atomics; the reference itself is), so they track, they do not coincide.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import neural_textures_amd as nt
+from neural_textures_amd import abi, params as P
+from helpers import make_state, rel_err, gpu_workspace
+from oracle_lib import load_oracle
+
+pytestmark = pytest.mark.gpu
+MLP_TOL = 1e-2
+CURVE_TOL = 0.10
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import torch
+    assert torch.cuda.is_available()
+    return nt.load()
+
+
+@pytest.fixture(scope="module")
+def O():
+    return load_oracle()
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def test_config1_catmull_rom_forward(lib, O):
+    import torch
+    say("case: config 1 (256^2 x 8 grid, 65,536 UVs, Catmull-Rom, 8-64-64-3)")
+    rng = np.random.default_rng(1337)
+    grid = P.make_grid(256, 256, 1, 8, rng, with_adam=False)
+    net = P.make_network([8, 64, 64, 3], used_outputs=3, rng=rng, init="xavier")
+    n = 65536
+    uvz = np.zeros((n, 3), np.float32)
+    uvz[:, :2] = np.random.default_rng(1338).uniform(0, 1, size=(n, 2))
+    lat = abi.nt_latents()
+    lat.num_grids, lat.channels = 1, 8
+    lat.grids[0] = grid.struct()
+    feats = np.zeros(n * 8, np.uint16)
+    outs = np.zeros(n * 3, np.uint16)
+    assert O.ntref_forward(C.byref(lat), C.byref(net.struct()), abi.NT_FILTER_CATMULL_ROM,
+                           uvz.ctypes.data, n, feats.ctypes.data, outs.ctypes.data) == 0
+    ggrid, gnet = grid.converted(True, "cuda"), net.converted(True, "cuda")
+    glat = abi.nt_latents()
+    glat.num_grids, glat.channels = 1, 8
+    glat.grids[0] = ggrid.struct()
+    guvz = torch.from_numpy(uvz).cuda()
+    gf = torch.zeros(n * 8, dtype=torch.int16, device="cuda")
+    go = torch.zeros(n * 3, dtype=torch.int16, device="cuda")
+    nt.check(lib.nt_forward(C.byref(glat), C.byref(gnet.struct()), abi.NT_FILTER_CATMULL_ROM,
+                            guvz.data_ptr(), n, gf.data_ptr(), go.data_ptr(), None))
+    torch.cuda.synchronize()
+    assert np.array_equal(gf.cpu().numpy().view(np.uint16), feats)
+    got = go.cpu().numpy().view(np.float16).astype(np.float32)
+    want = outs.view(np.float16).astype(np.float32)
+    err = rel_err(got, want)
+    say(f"config 1 output rel err {err:.2e}")
+    assert err <= MLP_TOL
+
+
+def smooth_textures(st, seed):
+    """Replaces the random targets of a state by smooth sinusoids (learnable targets)."""
+    rng = np.random.default_rng(seed)
+    h, w = st.image_height, st.image_width
+    y, x = np.mgrid[0:h, 0:w].astype(np.float64)
+    for t in st.textures:
+        data = np.zeros((h, w, t.pitch), np.float32)
+        for c in range(min(t.num_channels, t.pitch)):
+            fx, fy, ph = rng.integers(1, 4), rng.integers(1, 4), rng.uniform(0, 2 * np.pi)
+            data[:, :, c] = 0.5 + 0.4 * np.sin(2 * np.pi * (fx * x / w + fy * y / h) + ph)
+        t.texels = data.reshape(-1)
+
+
+def test_loss_curve_tracks_oracle(lib, O):
+    import torch
+    say("case: loss curve c2 shapes, 128^2 image, 32x32 region, 1000 steps")
+    steps, every, image = 1000, 200, 128
+    st = make_state("c2", image=image, region=(32, 32), seed=21, init="xavier")
+    smooth_textures(st, 22)
+    nch = 9
+    no = st.net.sizes[-1]
+    st.inference_output = np.zeros(image * image * no, np.float32)
+    st.inference_mse_accum = np.zeros(1, np.float32)
+    gs = gpu_workspace(lib, st.to_torch(), abi.NT_UNCONSTRAINED)
+    offs = np.random.default_rng(20260411).integers(0, image - 32 + 1, size=(steps, 2))
+    threads = max(1, min(16, os.cpu_count() or 1))
+    base_lr = 1e-2
+
+    def cpu_inf(s):
+        assert O.ntref_inference(C.byref(s.params())) == 0
+
+    def gpu_inf(s):
+        nt.check(lib.nt_inference(C.byref(s.params()), None))
+        torch.cuda.synchronize()
+
+    curve = []
+    for i in range(steps + 1):
+        if i % every == 0:
+            st.inference_mse_accum[:] = 0
+            cpu_inf(st)
+            c = float(st.inference_mse_accum[0]) / (image * image * nch)
+            gs.inference_mse_accum.zero_()
+            gpu_inf(gs)
+            g = float(gs.inference_mse_accum.cpu()[0]) / (image * image * nch)
+            curve.append((i, c, g))
+            say(f"step {i:5d}: oracle MSE {c:.6f}  gpu MSE {g:.6f}  ratio {g / c:.4f}")
+        if i == steps:
+            break
+        lr = np.float32(base_lr) * np.float32(0.9995) ** np.float32(i)
+        for s in (st, gs):
+            s.texel_offset_x, s.texel_offset_y = int(offs[i, 0]), int(offs[i, 1])
+            s.feature_adam = (0.9, 0.999, float(lr), 1e-8)
+        p = st.params()
+        assert O.ntref_train_step(C.byref(p), abi.NT_UNCONSTRAINED, threads) == 0
+        assert O.ntref_optimize_network(C.byref(p)) == 0
+        assert O.ntref_optimize_latents(C.byref(p), abi.NT_UNCONSTRAINED) == 0
+        gp = gs.params()
+        nt.check(lib.nt_train_step(C.byref(gp), abi.NT_UNCONSTRAINED, None))
+        nt.check(lib.nt_optimize_network(C.byref(gp), None))
+        nt.check(lib.nt_optimize_latents(C.byref(gp), abi.NT_UNCONSTRAINED, None))
+        st.step += 1
+        gs.step += 1
+    first, last = curve[0], curve[-1]
+    assert last[1] < 0.25 * first[1], "the oracle's loss must fall"
+    for i, c, g in curve:
+        assert abs(g - c) <= CURVE_TOL * c, f"step {i}: gpu {g} vs oracle {c}"

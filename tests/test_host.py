@@ -1,0 +1,58 @@
+"""The C++ host program (neural_textures_amd/host/nt_train): its host-only self-test on the
+CPU, and on the GPU a short run of the reference training loop (main.cpp:1017-1109) whose
+inference MSE must drop below the untrained network's."""
+import os
+import re
+import subprocess
+
+import pytest
+
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PROGRAM = os.path.join(ROOT, "neural_textures_amd", "host", "nt_train")
+
+
+@pytest.fixture(scope="module")
+def program():
+    if not os.path.exists(PROGRAM):
+        pytest.fail("host/nt_train is not built (run __graft_entry__.build())")
+    return PROGRAM
+
+
+def test_host_self_test(program):
+    out = subprocess.run([program, "--self-test"], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "self-test: ok" in out.stdout
+
+
+def test_host_rejects_bad_arguments(program):
+    out = subprocess.run([program, "--bogus"], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 2
+    assert "unknown option" in out.stderr
+
+
+def _mse(text, label):
+    m = re.search(label + r": ([0-9.eE+-]+)", text)
+    assert m, text
+    return float(m.group(1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("args", [
+    # the reference network: 4 grids x 3 channels of mode 0, 12 -> 32 -> 32 -> 16, 3 targets
+    ["--grids", "4", "--channels", "3", "--hidden", "32,32", "--targets", "3"],
+    # config 2 shapes: 2 grids x 16 channels, 32 -> 64 -> 64 -> 16 (9 used), 9 targets
+    ["--grids", "2", "--channels", "16", "--hidden", "64,64", "--targets", "9",
+     "--feature-lr", "1e-2", "--network-lr", "5e-3"],
+], ids=["ref", "c2"])
+def test_host_training_loop_reduces_mse(program, args):
+    cmd = [program, "--mode", "0", "--image", "512", "--iters", "300", "--progress", "100",
+           "--samples", "65536", *args]
+    print("running", " ".join(cmd), flush=True)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=110)
+    text = out.stdout + out.stderr
+    assert out.returncode == 0, text
+    assert "Completed iteration 300 / 300" in text
+    before, after = _mse(text, "Initial inference MSE"), _mse(text, "Inference MSE")
+    print(f"MSE {before:.6f} -> {after:.6f}", flush=True)
+    assert after == after and after < 0.5 * before, text
