@@ -287,7 +287,15 @@ typedef struct nt_decode_params {
     float mip_min;    /* mip coordinate z ~ U[mip_min, mip_max) */
     float mip_max;
     uint16_t *output; /* [pixel][mlp.used_outputs] fp16 */
+    /* Optional scratch (NULL: none). With nt_decode_workspace_bytes() bytes the decode runs
+     * in two passes: every block is first expanded once into fp16 texels, then the pixels
+     * sample those. Same results, fewer operations per pixel. 16-byte aligned. */
+    void *workspace;
+    size_t workspace_bytes;
 } nt_decode_params;
+
+/* Workspace bytes for the two-pass decode (0 on a bad argument). */
+size_t nt_decode_workspace_bytes(const nt_decode_params *params);
 
 /*
  * Decode a full image from codec-quantized latents: per pixel, jittered UV and random mip,

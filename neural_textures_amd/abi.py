@@ -111,6 +111,7 @@ class nt_decode_params(C.Structure):
         ("out_width", C.c_int), ("out_height", C.c_int),
         ("seed", C.c_uint32), ("jitter", C.c_float), ("mip_min", C.c_float), ("mip_max", C.c_float),
         ("output", u16p),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
     ]
 
 
@@ -135,6 +136,7 @@ SIGNATURES = {
     "nt_codec_mip_chain_layout": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, P(C.c_int64)]),
     "nt_codec_encode": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "nt_codec_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "nt_decode_workspace_bytes": (C.c_size_t, [P(nt_decode_params)]),
     "nt_decode": (C.c_int, [P(nt_decode_params), C.c_void_p]),
 }
 

@@ -5,6 +5,7 @@
 // instantiated for the network shape. Nothing here allocates device memory.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -254,8 +255,9 @@ int pack_targets(const nt_texture *tex, int ntex, int8_t *out_tex, int8_t *out_c
 struct TrainPlan {
     int shape, nwg, chunks_per_wg, tiles_x, P, stage1_blocks, rows_per_block;
     int fp_floats, fp_stride, tile_ok, scatter_mfma, scatter_split, scatter_off, w_rows, union_off;
+    int vbox_floats, vbox_off;
     size_t weight_bytes;
-    int fp_w[NT_MAX_GRIDS], fp_h[NT_MAX_GRIDS], fp_off[NT_MAX_GRIDS];
+    int fp_w[NT_MAX_GRIDS], fp_h[NT_MAX_GRIDS], fp_off[NT_MAX_GRIDS], vb_off[NT_MAX_GRIDS];
     int cb_w[NT_MAX_GRIDS], cb_h[NT_MAX_GRIDS], w_row0[NT_MAX_GRIDS];
     size_t lds, workspace;
 };
@@ -308,7 +310,7 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     // that neighbouring texels fall in different LDS banks.
     const int C = p->latents.channels;
     plan->fp_stride = C | 1;
-    int fp = 0, w_rows = 0;
+    int fp = 0, w_rows = 0, vb = 0;
     for (int gi = 0; gi < p->latents.num_grids; ++gi) {
         const nt_grid &g = p->latents.grids[gi];
         const double rx = (double)g.width / p->image_width, ry = (double)g.height / p->image_height;
@@ -316,6 +318,8 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         plan->fp_h[gi] = (int)std::ceil(kChunkH * ry) + 4;
         plan->fp_off[gi] = fp;
         fp += plan->fp_w[gi] * plan->fp_h[gi] * plan->fp_stride;
+        plan->vb_off[gi] = vb;
+        vb += plan->fp_w[gi] * plan->fp_h[gi];
         // Chunk cell box for the MFMA scatter: positions in [x, x + 16] x [y, y + 8].
         plan->cb_w[gi] = (int)std::ceil(kChunkW * rx) + 2;
         plan->cb_h[gi] = (int)std::ceil(kChunkH * ry) + 2;
@@ -347,9 +351,17 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->fp_floats = type == NT_UNCONSTRAINED ? fp : 0;
     if (plan->fp_floats && head + fp_bytes(plan->fp_floats) + union_bytes(false, false) > kMaxLds)
         plan->fp_floats = 0; // box does not fit: scatter straight to global memory
-    if (plan->tile_ok && head + fp_bytes(plan->fp_floats) + union_bytes(true, false) > kMaxLds)
+    // With 16 channels the latent values under the box are staged in LDS too, so the
+    // gathers read LDS instead of HBM.
+    plan->vbox_floats = plan->fp_floats > 0 && C == 16 ? vb * 16 : 0;
+    if (plan->vbox_floats &&
+        head + fp_bytes(plan->fp_floats) + fp_bytes(plan->vbox_floats) + union_bytes(false, false) > kMaxLds)
+        plan->vbox_floats = 0;
+    plan->vbox_off = (int)(head + fp_bytes(plan->fp_floats));
+    if (plan->tile_ok &&
+        head + fp_bytes(plan->fp_floats) + fp_bytes(plan->vbox_floats) + union_bytes(true, false) > kMaxLds)
         plan->tile_ok = 0;
-    const size_t base = head + fp_bytes(plan->fp_floats);
+    const size_t base = head + fp_bytes(plan->fp_floats) + fp_bytes(plan->vbox_floats);
     plan->union_off = (int)base;
     plan->scatter_mfma = 0;
     plan->scatter_split = 0;
@@ -468,6 +480,7 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
         d.grid[gi].fp_w = plan.fp_w[gi];
         d.grid[gi].fp_h = plan.fp_h[gi];
         d.grid[gi].fp_off = plan.fp_off[gi];
+        d.grid[gi].vb_off = plan.vb_off[gi];
         d.grid[gi].cb_w = plan.cb_w[gi];
         d.grid[gi].cb_h = plan.cb_h[gi];
         d.grid[gi].w_row0 = plan.w_row0[gi];
@@ -489,6 +502,8 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     d.chunks_per_wg = plan.chunks_per_wg;
     d.fp_floats = plan.fp_floats;
     d.fp_stride = plan.fp_stride;
+    d.vbox_floats = plan.vbox_floats;
+    d.vbox_off = plan.vbox_off;
     d.tile_ok = plan.tile_ok;
     d.scatter_mfma = plan.scatter_mfma;
     d.w_rows = plan.w_rows;
@@ -804,6 +819,33 @@ int nt_codec_decode(const void *blocks, int width, int height, int channels, flo
         "codec decode launch");
 }
 
+// Workspace of the two-pass decode: per grid its fp16 texel chain (32 bytes per texel at
+// 16 channels), each segment 256-byte aligned.
+static size_t decode_workspace_layout(const nt_decode_params *p, size_t *seg_off)
+{
+    size_t off = 0;
+    for (int gi = 0; gi < p->num_grids; ++gi) {
+        const nt_codec_grid &g = p->grids[gi];
+        int64_t mip_off[NT_MAX_MIPS];
+        const int64_t texels = nt_mip_chain_layout(g.width, g.height, g.num_mips, mip_off);
+        if (texels < 0)
+            return 0;
+        if (seg_off)
+            seg_off[gi] = off;
+        off += (((size_t)texels * (size_t)p->channels * 2) + 255) & ~(size_t)255;
+    }
+    return off;
+}
+
+size_t nt_decode_workspace_bytes(const nt_decode_params *p)
+{
+    if (!p || p->channels != 16 || p->num_grids < 1 || p->num_grids > NT_MAX_GRIDS) {
+        fail(NT_ERR_INVALID_ARGUMENT, "the two-pass decode needs 1..4 grids of 16 channels");
+        return 0;
+    }
+    return decode_workspace_layout(p, nullptr);
+}
+
 int nt_decode(const nt_decode_params *p, void *stream)
 {
     if (!p)
@@ -854,8 +896,47 @@ int nt_decode(const nt_decode_params *p, void *stream)
     d.jitter = p->jitter;
     d.mip_min = p->mip_min;
     d.mip_max = p->mip_max;
-    ProfileScope prof((hipStream_t)stream);
-    return hip_status(launch_forward(shape, kFwdDecode, d, (hipStream_t)stream), "decode launch");
+    hipStream_t s = (hipStream_t)stream;
+    if (p->workspace) {
+        // Two passes: expand every block once into fp16 texels, then sample those.
+        if (C != 16)
+            return fail(NT_ERR_UNSUPPORTED, "the two-pass decode is built for 16 channels per grid");
+        size_t seg[NT_MAX_GRIDS];
+        const size_t need = decode_workspace_layout(p, seg);
+        if (p->workspace_bytes < need)
+            return fail(NT_ERR_WORKSPACE, "decode workspace of %zu bytes needed, %zu given", need,
+                        p->workspace_bytes);
+        if (!aligned16(p->workspace))
+            return fail(NT_ERR_MISALIGNED, "decode workspace must be 16-byte aligned");
+        CodecExpandDesc x{};
+        int64_t items = 0;
+        for (int gi = 0; gi < p->num_grids; ++gi) {
+            const nt_codec_grid &g = p->grids[gi];
+            uint16_t *chain = (uint16_t *)((uint8_t *)p->workspace + seg[gi]);
+            nt_mip_chain_layout(g.width, g.height, g.num_mips, d.grid[gi].mip_off);
+            d.grid[gi].w = g.width;
+            d.grid[gi].h = g.height;
+            d.grid[gi].num_mips = g.num_mips;
+            d.half_values[gi] = chain;
+            for (int m = 0; m < g.num_mips; ++m) {
+                const int k = x.levels++;
+                const int w = std::max(g.width >> m, 1), h = std::max(g.height >> m, 1);
+                x.w[k] = w;
+                x.blocks[k] = (const uint8_t *)g.blocks + g.byte_offset[m];
+                x.out[k] = chain + d.grid[gi].mip_off[m] * 16;
+                x.start[k] = items;
+                items += (int64_t)w * h * 2;
+            }
+        }
+        x.start[x.levels] = items;
+        hipError_t e = launch_codec_expand(x, s);
+        if (e != hipSuccess)
+            return hip_status(e, "decode expand launch");
+        ProfileScope prof(s);
+        return hip_status(launch_forward(shape, kFwdDecode16, d, s), "decode launch");
+    }
+    ProfileScope prof(s);
+    return hip_status(launch_forward(shape, kFwdDecode, d, s), "decode launch");
 }
 
 } // extern "C"

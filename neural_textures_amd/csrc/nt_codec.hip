@@ -97,6 +97,49 @@ __global__ __launch_bounds__(256) void codec_decode_kernel(const uint8_t *blocks
     }
 }
 
+// Expand every mip of every codec grid into fp16 texels (the first pass of the two-pass
+// decode): one thread per (texel, 8 channels), one 16-byte store. Work items are numbered
+// over the concatenated (grid, mip) levels; level k starts at item d.start[k].
+__global__ __launch_bounds__(256) void codec_expand_kernel(CodecExpandDesc d)
+{
+    constexpr int C = 16, G8 = C / 8;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= d.start[d.levels])
+        return;
+    int k = 0;
+    for (int j = 1; j < d.levels; ++j)
+        k = i >= d.start[j] ? j : k;
+    const int64_t local = i - d.start[k];
+    const int W = d.w[k];
+    const int64_t texel = local / G8;
+    const int cg = (int)(local % G8);
+    const int x = (int)(texel % W), y = (int)(texel / W);
+    const uint8_t *rec = d.blocks[k] + ((int64_t)(y >> 2) * ((W + 3) >> 2) + (x >> 2)) * (12 * C);
+    const int pix = ((y & 3) << 2) + (x & 3);
+    const uint4 e0 = *(const uint4 *)(rec + 32 * cg);
+    const uint4 e1 = *(const uint4 *)(rec + 32 * cg + 16);
+    const uint32_t idx = *(const uint32_t *)(rec + 4 * C + pix * (C / 2) + 4 * cg);
+    const uint32_t ends[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+    uint32_t packed[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const uint32_t lo = codec_unkey(codec_interp(ends[e] & 0xFFFFu, ends[e] >> 16, (idx >> (4 * e)) & 15));
+        const uint32_t hi =
+            codec_unkey(codec_interp(ends[e + 1] & 0xFFFFu, ends[e + 1] >> 16, (idx >> (4 * e + 4)) & 15));
+        packed[e / 2] = lo | (hi << 16);
+    }
+    *(uint4 *)(d.out[k] + texel * C + 8 * cg) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+}
+
+hipError_t launch_codec_expand(const CodecExpandDesc &d, hipStream_t s)
+{
+    const int64_t total = d.start[d.levels];
+    if (total <= 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(codec_expand_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
 template <int C>
 static hipError_t encode_c(const float *values, int w, int h, uint8_t *blocks, hipStream_t s)
 {

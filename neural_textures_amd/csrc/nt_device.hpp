@@ -35,6 +35,30 @@ __device__ __forceinline__ float rn32(float x)
 // fp32 -> fp16 of an fp32 product, with the product rounded to fp32 first.
 __device__ __forceinline__ _Float16 half_of_product(float a, float b) { return (_Float16)rn32(a * b); }
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+// acc[e] = acc[e] + (half)(w * v[e]) for eight channels, with the same two roundings per
+// term as half_of_product + v_add_f16, two channels per instruction: fp32 products,
+// v_cvt_pk_f16_f32 (round to nearest even) and v_pk_add_f16 (correctly rounded).
+__device__ __forceinline__ h8 accumulate_products(h8 acc, float w, float4 a, float4 b)
+{
+    const f2 p0 = {rn32(w * a.x), rn32(w * a.y)}, p1 = {rn32(w * a.z), rn32(w * a.w)};
+    const f2 p2 = {rn32(w * b.x), rn32(w * b.y)}, p3 = {rn32(w * b.z), rn32(w * b.w)};
+    const h2 q0 = __builtin_convertvector(p0, h2), q1 = __builtin_convertvector(p1, h2);
+    const h2 q2 = __builtin_convertvector(p2, h2), q3 = __builtin_convertvector(p3, h2);
+    const h8 q = __builtin_shufflevector(__builtin_shufflevector(q0, q1, 0, 1, 2, 3),
+                                         __builtin_shufflevector(q2, q3, 0, 1, 2, 3), 0, 1, 2, 3, 4,
+                                         5, 6, 7);
+    return acc + q;
+}
+// The same for eight fp16 values (each widened to fp32 exactly before the product).
+__device__ __forceinline__ h8 accumulate_products(h8 acc, float w, h8 v)
+{
+    return accumulate_products(acc, w, make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]),
+                               make_float4((float)v[4], (float)v[5], (float)v[6], (float)v[7]));
+}
+
 __device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)bits_h(b); }

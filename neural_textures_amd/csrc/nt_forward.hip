@@ -19,6 +19,13 @@ struct FwdLayout {
     static constexpr int bytes = frag_bytes + ((S::bias_total() * 4 + 15) / 16) * 16;
 };
 
+// Corner coordinate wrap for positions clamped into the image: every bilinear corner lies
+// in [-1, size], so one compare per side replaces the modulo of wrap_coord.
+__device__ __forceinline__ int wrap_edge(int c, int size)
+{
+    return c < 0 ? c + size : (c >= size ? c - size : c);
+}
+
 // Mip pair for mip coordinate z (train.cu:266-281).
 __device__ __forceinline__ int mip_pair(int num_mips, float z, int (&mips)[2], float (&w)[2])
 {
@@ -167,7 +174,7 @@ __device__ __forceinline__ void sample_codec(const FwdDesc &d, float u, float v,
             const uint8_t *base = gr.blocks + gr.byte_off[mips[mi]];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int tx = wrap_coord(f.x0 + (c & 1), w), ty = wrap_coord(f.y0 + (c >> 1), h);
+                const int tx = wrap_edge(f.x0 + (c & 1), w), ty = wrap_edge(f.y0 + (c >> 1), h);
                 const uint8_t *rec = base + ((int64_t)(ty >> 2) * bw + (tx >> 2)) * (12 * C);
                 const int pix = ((ty & 3) << 2) + (tx & 3);
                 const uint4 e01 = *(const uint4 *)(rec + 4 * cb);
@@ -182,6 +189,39 @@ __device__ __forceinline__ void sample_codec(const FwdDesc &d, float u, float v,
                 }
             }
         }
+    }
+}
+
+// Trilinear sample of the expanded fp16 texels (16 channels per grid; lane group g takes
+// channels 8g .. 8g+7 of every grid). The texel values are the codec's decoded fp16
+// numbers, so the result equals sample_codec's bit for bit.
+template <int KQ>
+__device__ __forceinline__ void sample_half16(const FwdDesc &d, float u, float v, float z, int g,
+                                              h8 (&x)[KQ])
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+        h8 acc = (h8)(_Float16)0.f;
+        if (q < d.G) {
+            const GridDesc &gr = d.grid[q];
+            int mips[2];
+            float mw[2];
+            const int nm = mip_pair(gr.num_mips, z, mips, mw);
+            for (int mi = 0; mi < nm; ++mi) {
+                const int w = mip_dim(gr.w, mips[mi]), h = mip_dim(gr.h, mips[mi]);
+                const Footprint f = bilinear_footprint(u, v, w, h, mw[mi]);
+                const uint4 *base = (const uint4 *)(d.half_values[q] + gr.mip_off[mips[mi]] * 16) + g;
+                const int x0 = wrap_edge(f.x0, w), x1 = wrap_edge(f.x0 + 1, w);
+                const int r0 = wrap_edge(f.y0, h) * w, r1 = wrap_edge(f.y0 + 1, h) * w;
+                const uint4 t0 = base[2 * (r0 + x0)], t1 = base[2 * (r0 + x1)];
+                const uint4 t2 = base[2 * (r1 + x0)], t3 = base[2 * (r1 + x1)];
+                acc = accumulate_products(acc, f.w[0], __builtin_bit_cast(h8, t0));
+                acc = accumulate_products(acc, f.w[1], __builtin_bit_cast(h8, t1));
+                acc = accumulate_products(acc, f.w[2], __builtin_bit_cast(h8, t2));
+                acc = accumulate_products(acc, f.w[3], __builtin_bit_cast(h8, t3));
+            }
+        }
+        x[q] = acc;
     }
 }
 
@@ -229,7 +269,7 @@ __global__ __launch_bounds__(kFwdThreads) void forward_kernel(FwdDesc d)
             u = ((float)px + 0.5f) / (float)d.image_w; // train.cu:926-933
             v = ((float)py + 0.5f) / (float)d.image_h;
             sample_bilinear<C, KQ0>(d, u, v, 0.f, g, x0);
-        } else { // kFwdDecode
+        } else { // kFwdDecode, kFwdDecode16
             const int sc = valid ? s : 0;
             const int px = sc % d.image_w, py = sc / d.image_w;
             uint32_t st = mix_seed((uint32_t)sc, d.seed);
@@ -241,7 +281,10 @@ __global__ __launch_bounds__(kFwdThreads) void forward_kernel(FwdDesc d)
             u = posx / (float)d.image_w;
             v = posy / (float)d.image_h;
             const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
-            sample_codec<C, KQ0>(d, u, v, z, g, x0);
+            if constexpr (MODE == kFwdDecode16)
+                sample_half16<KQ0>(d, u, v, z, g, x0);
+            else
+                sample_codec<C, KQ0>(d, u, v, z, g, x0);
         }
         if (d.features != nullptr && valid) {
             const int nf = d.G * C;
@@ -374,6 +417,10 @@ static hipError_t launch_modes(int mode, const FwdDesc &d, hipStream_t s)
     case kFwdDecode:
         if constexpr (C == 16 || C == 8)
             return launch_fwd<S, C, kFwdDecode>(d, s);
+        return hipErrorInvalidValue;
+    case kFwdDecode16:
+        if constexpr (C == 16)
+            return launch_fwd<S, C, kFwdDecode16>(d, s);
         return hipErrorInvalidValue;
     default:
         return hipErrorInvalidValue;

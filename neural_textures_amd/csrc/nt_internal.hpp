@@ -32,6 +32,7 @@ struct GridDesc {
     float *block_grads;
     int w, h, num_mips;
     int fp_w, fp_h, fp_off; // train kernel: LDS footprint box and offset (floats)
+    int vb_off;             // train kernel: first texel of this grid in the LDS value box
     int cb_w, cb_h, w_row0; // train kernel: chunk cell box and its first row in the scatter matrices
     int64_t mip_off[NT_MAX_MIPS];   // texels
     int64_t block_off[NT_MAX_MIPS]; // blocks
@@ -56,6 +57,8 @@ struct TrainDesc {
     int tiles_x, chunks_per_wg;
     int fp_floats;  // LDS footprint floats (0: scatter straight to global)
     int fp_stride;  // floats per texel in the footprint box (odd: spreads texels over banks)
+    int vbox_floats; // LDS copy of the latent values under the footprint box (C = 16; 0: gather from HBM)
+    int vbox_off;    // its byte offset in LDS
     int tile_ok;    // the chunk's target taps are staged in LDS (textures match the image size)
     int scatter_mfma; // latent scatter as an MFMA reduction over the chunk (else LDS atomics)
     int w_rows;     // rows of each bilinear-weight matrix (all grids, 16-row tiles)
@@ -85,12 +88,29 @@ struct ReduceDesc {
     float *bgrad[NT_MAX_LAYERS];
 };
 
-enum FwdMode { kFwdMlp = 0, kFwdBilinear = 1, kFwdCatmullRom = 2, kFwdInference = 3, kFwdDecode = 4 };
+enum FwdMode {
+    kFwdMlp = 0,
+    kFwdBilinear = 1,
+    kFwdCatmullRom = 2,
+    kFwdInference = 3,
+    kFwdDecode = 4,   // samples codec blocks directly
+    kFwdDecode16 = 5  // samples the fp16 texels of the first decode pass
+};
 
 struct CodecGrid {
     const uint8_t *blocks;
     int w, h, num_mips;
     int64_t byte_off[NT_MAX_MIPS];
+};
+
+// First pass of the two-pass decode: codec blocks of every (grid, mip) level -> fp16 texels.
+constexpr int kMaxExpandLevels = NT_MAX_GRIDS * NT_MAX_MIPS;
+struct CodecExpandDesc {
+    int levels;
+    int w[kMaxExpandLevels];
+    const uint8_t *blocks[kMaxExpandLevels];
+    uint16_t *out[kMaxExpandLevels];
+    int64_t start[kMaxExpandLevels + 1]; // prefix of work items (texels x 2)
 };
 
 // Forward-only passes: nt_mlp_forward, nt_forward, nt_inference, nt_decode.
@@ -104,6 +124,7 @@ struct FwdDesc {
     int G, C, ntex;
     int count; // samples (pixels)
     int image_w, image_h;
+    const uint16_t *half_values[NT_MAX_GRIDS]; // kFwdDecode16: expanded fp16 texel chains
     const uint16_t *inputs; // kFwdMlp
     const float *uvz;       // kFwdBilinear / kFwdCatmullRom
     uint16_t *features;     // optional fp16 features
@@ -167,5 +188,6 @@ hipError_t launch_codec_encode(const float *values, int w, int h, int C, uint8_t
                                hipStream_t s);
 hipError_t launch_codec_decode(const uint8_t *blocks, int w, int h, int C, float *values,
                                hipStream_t s);
+hipError_t launch_codec_expand(const CodecExpandDesc &d, hipStream_t s);
 
 } // namespace ntk

@@ -162,6 +162,78 @@ __device__ __forceinline__ void gather_unconstrained(const TrainDesc &d, const S
     }
 }
 
+// Copy the latent values under every grid's footprint box into LDS (16 channels: four
+// float4 per texel, texel (lx, ly) of grid gi at vbox[(vb_off + ly * fp_w + lx) * 16]).
+// Box texels map to the grid with wrap addressing, as the gathers do.
+template <int GM>
+__device__ __forceinline__ void load_value_box(const TrainDesc &d, float4 *vbox,
+                                               const int (&flo_x)[NT_MAX_GRIDS],
+                                               const int (&flo_y)[NT_MAX_GRIDS], int tid)
+{
+#pragma unroll
+    for (int gi = 0; gi < GM; ++gi) {
+        const GridDesc &gr = d.grid[gi];
+        if (gi >= d.G)
+            break;
+        const int n4 = gr.fp_w * gr.fp_h * 4;
+        float4 *dst = vbox + gr.vb_off * 4;
+        for (int i = tid; i < n4; i += kTrainThreads) {
+            const int texel = i >> 2, part = i & 3;
+            const int lx = texel % gr.fp_w, ly = texel / gr.fp_w;
+            const int gx = wrap_coord(flo_x[gi] + lx, gr.w), gy = wrap_coord(flo_y[gi] + ly, gr.h);
+            dst[i] = ((const float4 *)(gr.values + ((int64_t)gy * gr.w + gx) * 16))[part];
+        }
+    }
+}
+
+// The 16-channel gather of gather_unconstrained reading the LDS value box (same products
+// and fp16 accumulation order); corners outside the box (never expected: the box has a
+// texel of slack on every side) read HBM.
+template <int KQ>
+__device__ __forceinline__ void gather_box16(const TrainDesc &d, const SampleFootprints &f,
+                                             const int (&flo_x)[NT_MAX_GRIDS],
+                                             const int (&flo_y)[NT_MAX_GRIDS], const float *vbox,
+                                             int g, h8 (&x)[KQ])
+{
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+        h8 acc;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            acc[e] = (_Float16)0.f;
+        if (q < d.G) {
+            const GridDesc &gr = d.grid[q];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int tx = f.x0[q] + (c & 1), ty = f.y0[q] + (c >> 1);
+                const int lx = tx - flo_x[q], ly = ty - flo_y[q];
+                float4 a, b;
+                if (lx >= 0 && lx < gr.fp_w && ly >= 0 && ly < gr.fp_h) {
+                    const float4 *p = (const float4 *)(vbox + (gr.vb_off + ly * gr.fp_w + lx) * 16 + 8 * g);
+                    a = p[0];
+                    b = p[1];
+                } else {
+                    const float4 *p = (const float4 *)(gr.values +
+                                                       ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * 16 +
+                                                       8 * g);
+                    a = p[0];
+                    b = p[1];
+                }
+                const float wc = f.w[q][c];
+                acc[0] = acc[0] + half_of_product(wc, a.x);
+                acc[1] = acc[1] + half_of_product(wc, a.y);
+                acc[2] = acc[2] + half_of_product(wc, a.z);
+                acc[3] = acc[3] + half_of_product(wc, a.w);
+                acc[4] = acc[4] + half_of_product(wc, b.x);
+                acc[5] = acc[5] + half_of_product(wc, b.y);
+                acc[6] = acc[6] + half_of_product(wc, b.z);
+                acc[7] = acc[7] + half_of_product(wc, b.w);
+            }
+        }
+        x[q] = acc;
+    }
+}
+
 // BC6 block record of texel (x, y) at mip 0 (train.cu:204-212, 240-261).
 struct Bc6Texel {
     int64_t block;
@@ -707,6 +779,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
     }
     for (int i = tid; i < d.fp_floats; i += kTrainThreads)
         fp[i] = 0.f;
+    float *vbox = (float *)(smem + d.vbox_off);
 
     const int tile_x = blockIdx.x % d.tiles_x, tile_y = blockIdx.x / d.tiles_x;
     const int tx0 = tile_x * kChunkW * d.chunks_per_wg, ty0 = tile_y * kChunkH;
@@ -717,6 +790,10 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
         const GridDesc &gr = d.grid[gi];
         flo_x[gi] = gi < GM ? (int)floorf((float)(d.off_x + tx0) * (float)gr.w / (float)d.image_w - 0.5f) - 1 : 0;
         flo_y[gi] = gi < GM ? (int)floorf((float)(d.off_y + ty0) * (float)gr.h / (float)d.image_h - 0.5f) - 1 : 0;
+    }
+    if constexpr (C == 16 && TYPE == NT_UNCONSTRAINED) {
+        if (d.vbox_floats > 0)
+            load_value_box<GM>(d, (float4 *)vbox, flo_x, flo_y, tid);
     }
 
     f16v dwacc[LY::slots];
@@ -760,7 +837,12 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
             SampleFootprints fps;
             sample_footprints<GM>(d, u, v, fps);
             if (valid) {
-                if constexpr (TYPE == NT_UNCONSTRAINED)
+                if constexpr (TYPE == NT_UNCONSTRAINED && C == 16) {
+                    if (d.vbox_floats > 0)
+                        gather_box16<KQ0>(d, fps, flo_x, flo_y, vbox, g, x0);
+                    else
+                        gather_unconstrained<C, KQ0>(d, fps, g, x0);
+                } else if constexpr (TYPE == NT_UNCONSTRAINED)
                     gather_unconstrained<C, KQ0>(d, fps, g, x0);
                 else
                     gather_bc6<C, KQ0>(d, fps, g, x0);

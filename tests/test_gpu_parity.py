@@ -325,3 +325,16 @@ def test_decode_from_codec_latents(lib, O):
     sync()
     got = gout.cpu().numpy().view(np.float16).astype(np.float32)
     assert rel_err(got, want.view(np.float16).astype(np.float32)) <= MLP_TOL
+    # The two-pass decode (blocks expanded to fp16 texels first) gives the same bits.
+    say("case: decode c4 two-pass")
+    nbytes = lib.nt_decode_workspace_bytes(C.byref(gp))
+    assert nbytes > 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    gout2 = torch.zeros_like(gout)
+    gp2 = dparams([g.data_ptr() for g in gblobs], gnet, gout2.data_ptr())
+    gp2.workspace, gp2.workspace_bytes = ws.data_ptr(), nbytes
+    nt.check(lib.nt_decode(C.byref(gp2), None))
+    sync()
+    assert torch.equal(gout2, gout)
+    gp2.workspace_bytes = nbytes - 16
+    assert lib.nt_decode(C.byref(gp2), None) == abi.NT_ERR_WORKSPACE
