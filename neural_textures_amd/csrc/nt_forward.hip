@@ -71,16 +71,7 @@ __device__ __forceinline__ void sample_bilinear(const FwdDesc &d, float u, float
                 for (int c = 0; c < 4; ++c) {
                     const int tx = wrap_coord(f.x0 + (c & 1), w), ty = wrap_coord(f.y0 + (c >> 1), h);
                     const float4 *p = (const float4 *)(vals + ((int64_t)ty * w + tx) * C);
-                    const float4 a = p[0], b = p[1];
-                    const float wc = f.w[c];
-                    x[q][0] = x[q][0] + half_of_product(wc, a.x);
-                    x[q][1] = x[q][1] + half_of_product(wc, a.y);
-                    x[q][2] = x[q][2] + half_of_product(wc, a.z);
-                    x[q][3] = x[q][3] + half_of_product(wc, a.w);
-                    x[q][4] = x[q][4] + half_of_product(wc, b.x);
-                    x[q][5] = x[q][5] + half_of_product(wc, b.y);
-                    x[q][6] = x[q][6] + half_of_product(wc, b.z);
-                    x[q][7] = x[q][7] + half_of_product(wc, b.w);
+                    x[q] = accumulate_products(x[q], f.w[c], p[0], p[1]);
                 }
             }
         } else {
@@ -225,8 +216,13 @@ __device__ __forceinline__ void sample_half16(const FwdDesc &d, float u, float v
     }
 }
 
+// Decode keeps its per-tile state within 128 VGPRs, so it asks for four waves per SIMD
+// (16 per CU) to hide the gather latency; the other modes keep the default.
+template <int MODE>
+constexpr int fwd_min_blocks() { return MODE == kFwdDecode || MODE == kFwdDecode16 ? 4 : 1; }
+
 template <class S, int C, int MODE>
-__global__ __launch_bounds__(kFwdThreads) void forward_kernel(FwdDesc d)
+__global__ __launch_bounds__(kFwdThreads, fwd_min_blocks<MODE>()) void forward_kernel(FwdDesc d)
 {
     using LY = FwdLayout<S>;
     constexpr int L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
@@ -373,11 +369,23 @@ __global__ __launch_bounds__(kFwdThreads) void forward_kernel(FwdDesc d)
                 }
             }
         } else {
+            // Lane group g holds output rows 4g .. 4g+3 and 8+4g .. 8+4g+3: with a row stride
+            // that is a multiple of 4 each run of four is one 8-byte store.
+            uint16_t *orow = d.out16 + (int64_t)s * d.out_stride;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int o = chained_feature(0, g, e);
-                if (o < d.out_stride)
-                    d.out16[(int64_t)s * d.out_stride + o] = h_bits((_Float16)out[0][e]);
+            for (int j = 0; j < 2; ++j) {
+                const int o = 8 * j + 4 * g;
+                const f2 v0 = {out[0][4 * j], out[0][4 * j + 1]}, v1 = {out[0][4 * j + 2], out[0][4 * j + 3]};
+                const h2 h0 = __builtin_convertvector(v0, h2), h1 = __builtin_convertvector(v1, h2);
+                if ((d.out_stride & 3) == 0 && o + 3 < d.out_stride) {
+                    *(uint2 *)(orow + o) = make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
+                } else {
+                    const _Float16 hv[4] = {h0[0], h0[1], h1[0], h1[1]};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (o + r < d.out_stride)
+                            orow[o + r] = h_bits(hv[r]);
+                }
             }
         }
     }

@@ -181,11 +181,15 @@ __device__ __forceinline__ void to_fragments(const f16v (&acc)[NA], h8 (&y)[NQ])
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = acc[q >> 1][8 * (q & 1) + e];
-            if (RELU)
-                v = v > 0.f ? v : 0.f;
-            y[q][e] = (_Float16)v;
+        for (int e = 0; e < 8; e += 2) {
+            f2 v = {acc[q >> 1][8 * (q & 1) + e], acc[q >> 1][8 * (q & 1) + e + 1]};
+            if (RELU) {
+                v[0] = v[0] > 0.f ? v[0] : 0.f;
+                v[1] = v[1] > 0.f ? v[1] : 0.f;
+            }
+            const h2 h = __builtin_convertvector(v, h2); // v_cvt_pk_f16_f32
+            y[q][e] = h[0];
+            y[q][e + 1] = h[1];
         }
     }
 }

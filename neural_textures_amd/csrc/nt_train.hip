@@ -125,16 +125,7 @@ __device__ __forceinline__ void gather_unconstrained(const TrainDesc &d, const S
                     const int tx = wrap_near(x0 + (c & 1), gw);
                     const int ty = wrap_near(y0 + (c >> 1), gh);
                     const float4 *p = (const float4 *)(vals + ((int64_t)ty * gw + tx) * C + cb);
-                    const float4 a = p[0], b = p[1];
-                    const float wc = w[c];
-                    acc[0] = acc[0] + half_of_product(wc, a.x);
-                    acc[1] = acc[1] + half_of_product(wc, a.y);
-                    acc[2] = acc[2] + half_of_product(wc, a.z);
-                    acc[3] = acc[3] + half_of_product(wc, a.w);
-                    acc[4] = acc[4] + half_of_product(wc, b.x);
-                    acc[5] = acc[5] + half_of_product(wc, b.y);
-                    acc[6] = acc[6] + half_of_product(wc, b.z);
-                    acc[7] = acc[7] + half_of_product(wc, b.w);
+                    acc = accumulate_products(acc, w[c], p[0], p[1]);
                 }
             }
         } else {
@@ -219,15 +210,7 @@ __device__ __forceinline__ void gather_box16(const TrainDesc &d, const SampleFoo
                     a = p[0];
                     b = p[1];
                 }
-                const float wc = f.w[q][c];
-                acc[0] = acc[0] + half_of_product(wc, a.x);
-                acc[1] = acc[1] + half_of_product(wc, a.y);
-                acc[2] = acc[2] + half_of_product(wc, a.z);
-                acc[3] = acc[3] + half_of_product(wc, a.w);
-                acc[4] = acc[4] + half_of_product(wc, b.x);
-                acc[5] = acc[5] + half_of_product(wc, b.y);
-                acc[6] = acc[6] + half_of_product(wc, b.z);
-                acc[7] = acc[7] + half_of_product(wc, b.w);
+                acc = accumulate_products(acc, f.w[q][c], a, b);
             }
         }
         x[q] = acc;
