@@ -260,9 +260,120 @@ struct TrainPlan {
     int fp_w[NT_MAX_GRIDS], fp_h[NT_MAX_GRIDS], fp_off[NT_MAX_GRIDS], vb_off[NT_MAX_GRIDS];
     int cb_w[NT_MAX_GRIDS], cb_h[NT_MAX_GRIDS], w_row0[NT_MAX_GRIDS];
     size_t lds, workspace;
+    // The 16-channel unconstrained kernel (nt_train16.hip), when it applies.
+    int use16, groups, rows;
+    Train16Desc t16;
 };
 
 constexpr size_t kMaxLds = 160 * 1024;
+
+// Plan of the 16-channel kernel (nt_train16.hip): unconstrained latents of 16 channels,
+// one to four reference textures of the image size with float4 texels (their channels
+// become output rows 4t + ch), and an LDS layout that fits. Sets plan->use16.
+void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
+{
+    plan->use16 = 0;
+    const int NG = train16_groups(plan->shape);
+    const int C = p->latents.channels, G = p->latents.num_grids;
+    if (type != NT_UNCONSTRAINED || C != 16 || NG == 0 || p->num_textures < 1 || p->num_textures > 4)
+        return;
+    Train16Desc &d = plan->t16;
+    d = Train16Desc{};
+    int prefix = 0;
+    bool mapped[NT_MAX_OUTPUTS] = {};
+    int8_t row_out[NT_MAX_OUTPUTS];
+    for (int r = 0; r < NT_MAX_OUTPUTS; ++r)
+        row_out[r] = -1;
+    for (int t = 0; t < p->num_textures; ++t) {
+        const nt_texture &x = p->textures[t];
+        if (!x.texels || x.num_channels < 1 || x.pitch != 4 || x.width != p->image_width ||
+            x.height != p->image_height || !aligned16(x.texels + x.mip_offset[0] * 4))
+            return;
+        const int nch = x.num_channels < 4 ? x.num_channels : 4;
+        d.tex[t] = x.texels + x.mip_offset[0] * 4;
+        d.tex_nch[t] = nch;
+        d.tex_w[t] = x.loss_weight;
+        for (int ch = 0; ch < nch; ++ch) {
+            row_out[4 * t + ch] = (int8_t)(prefix + ch);
+            mapped[prefix + ch] = true;
+        }
+        prefix += nch;
+    }
+    for (int t = p->num_textures; t < 4; ++t) {
+        d.tex[t] = d.tex[0];
+        d.tex_w[t] = 1.f;
+    }
+    // Rows without a texture channel take the remaining outputs in increasing order.
+    int next = 0;
+    for (int r = 0; r < NT_MAX_OUTPUTS; ++r) {
+        if (row_out[r] < 0) {
+            while (mapped[next])
+                ++next;
+            row_out[r] = (int8_t)next;
+            mapped[next] = true;
+        }
+        d.perm[r] = row_out[r];
+    }
+    d.ntex = p->num_textures;
+    const int rw = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
+    const int rows = (int)(((int64_t)p->num_samples + rw - 1) / rw);
+    d.tiles_x = (rw + 4 * kChunkW - 1) / (4 * kChunkW);
+    const int tiles_y = (rows + kChunkH * NG - 1) / (kChunkH * NG);
+    if ((int64_t)d.tiles_x * tiles_y > (1 << 30))
+        return;
+    d.nwg = d.tiles_x * tiles_y;
+    d.xcd_per = d.nwg % 8 == 0 ? d.nwg / 8 : 0;
+    int fp = 0, wcols = 0;
+    for (int gi = 0; gi < G; ++gi) {
+        const nt_grid &g = p->latents.grids[gi];
+        Grid16 &q = d.grid[gi];
+        const double rx = (double)g.width / p->image_width, ry = (double)g.height / p->image_height;
+        q.values = g.values + g.mip_offset[0] * C;
+        q.grads = g.grads + g.mip_offset[0] * C;
+        q.w = g.width;
+        q.h = g.height;
+        q.fp_w = (int)std::ceil(4 * kChunkW * rx) + 4;
+        q.fp_h = (int)std::ceil(kChunkH * NG * ry) + 4;
+        q.fp_off = fp;
+        fp += q.fp_w * q.fp_h * 16;
+        q.cb_w = (int)std::ceil(kChunkW * rx) + 2;
+        q.cb_h = (int)std::ceil(kChunkH * ry) + 2;
+        q.ncell = q.cb_w * q.cb_h;
+        q.wcol0 = wcols;
+        wcols += 16 * ((q.ncell + 15) / 16);
+        q.inv_cb_w = 1.f / (float)q.cb_w;
+        q.inv_fp_w = 1.f / (float)q.fp_w;
+        if (!aligned16(q.values) || !aligned16(q.grads))
+            return;
+    }
+    d.fp_floats = fp;
+    d.wcols = wcols;
+    const size_t head = train16_head_bytes(plan->shape);
+    const size_t scatter = ((size_t)p->mlp.sizes[0] * kRowStride + 2 * (size_t)kChunk * wcols) * 2;
+    size_t un = train16_transpose_bytes(plan->shape);
+    un = scatter > un ? scatter : un;
+    d.tile_bytes = d.ntex * kTileW * kTileH * 16;
+    d.group_bytes = (int)((d.tile_bytes + un + 15) & ~(size_t)15);
+    d.group_off = (int)((head + (size_t)fp * 4 + 15) & ~(size_t)15);
+    const size_t lds = (size_t)d.group_off + (size_t)NG * d.group_bytes;
+    if (lds > kMaxLds)
+        return;
+    plan->use16 = 1;
+    plan->groups = NG;
+    plan->lds = lds;
+    plan->nwg = d.nwg;
+    plan->rows = d.nwg * NG;
+    plan->stage1_blocks = (plan->rows + plan->rows_per_block - 1) / plan->rows_per_block;
+    plan->workspace = plan->weight_bytes +
+                      ((size_t)plan->rows + (size_t)plan->stage1_blocks) * (size_t)plan->P * sizeof(float);
+    d.image_w = p->image_width;
+    d.image_h = p->image_height;
+    d.off_x = p->texel_offset_x;
+    d.off_y = p->texel_offset_y;
+    d.region_w = rw;
+    d.num_samples = p->num_samples;
+    d.step = (uint32_t)p->step;
+}
 
 int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
 {
@@ -379,6 +490,8 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             plan->lds = base + union_bytes(plan->tile_ok, true);
         }
     }
+    plan->rows = plan->nwg;
+    plan16(p, type, plan);
     return NT_OK;
 }
 
@@ -466,7 +579,30 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
                     p->workspace ? p->workspace_bytes : (size_t)0);
     if (!aligned16(p->workspace))
         return fail(NT_ERR_MISALIGNED, "workspace must be 16-byte aligned");
-
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t *ws = (uint8_t *)p->workspace;
+    float *partial = (float *)(ws + plan.weight_bytes);
+    hipError_t e;
+    if (plan.use16) {
+        Prep16Desc prep{};
+        prep.mlp = mlp_desc(&p->mlp);
+        memcpy(prep.perm, plan.t16.perm, sizeof(prep.perm));
+        prep.frags = (uint4 *)ws;
+        prep.bias = (float *)(ws + train_frag_bytes(plan.shape));
+        Train16Desc d = plan.t16;
+        d.wfrags = prep.frags;
+        d.wbias = prep.bias;
+        d.partial = partial;
+        e = launch_prep16(plan.shape, prep, s);
+        if (e != hipSuccess)
+            return hip_status(e, "weight preparation launch");
+        {
+            ProfileScope prof(s);
+            e = launch_train16(plan.shape, d, plan.lds, s);
+        }
+        if (e != hipSuccess)
+            return hip_status(e, "train kernel launch");
+    } else {
     TrainDesc d{};
     d.mlp = mlp_desc(&p->mlp);
     const int C = p->latents.channels;
@@ -511,17 +647,15 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     d.scatter_split = plan.scatter_split;
     d.scatter_off = plan.scatter_off;
     // Workspace: weight fragments | fp32 biases | per-workgroup partials | reduction rows.
-    uint8_t *ws = (uint8_t *)p->workspace;
     PrepDesc prep{};
     prep.mlp = d.mlp;
     prep.frags = (uint4 *)ws;
     prep.bias = (float *)(ws + train_frag_bytes(plan.shape));
     d.wfrags = prep.frags;
     d.wbias = prep.bias;
-    d.partial = (float *)(ws + plan.weight_bytes);
+    d.partial = partial;
 
-    hipStream_t s = (hipStream_t)stream;
-    hipError_t e = launch_prep_weights(plan.shape, prep, s);
+    e = launch_prep_weights(plan.shape, prep, s);
     if (e != hipSuccess)
         return hip_status(e, "weight preparation launch");
     {
@@ -530,11 +664,12 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     }
     if (e != hipSuccess)
         return hip_status(e, "train kernel launch");
+    }
 
     ReduceDesc r{};
-    r.partial = d.partial;
-    r.tmp = d.partial + (size_t)plan.nwg * plan.P;
-    r.rows = plan.nwg;
+    r.partial = partial;
+    r.tmp = partial + (size_t)plan.rows * plan.P;
+    r.rows = plan.rows;
     r.rows_per_block = plan.rows_per_block;
     r.P = plan.P;
     r.stage1_blocks = plan.stage1_blocks;

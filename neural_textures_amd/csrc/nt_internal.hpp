@@ -70,6 +70,42 @@ struct TrainDesc {
     float *partial; // [gridDim.x][grad_total] per-workgroup MLP gradient partials
 };
 
+// The 16-channel unconstrained train kernel (nt_train16.hip).
+struct Grid16 {
+    const float *values; // mip 0, [texel][16]
+    float *grads;
+    int w, h;
+    int fp_w, fp_h, fp_off; // workgroup footprint box in LDS: [fp_h][fp_w][16] floats at fp_off
+    int cb_w, cb_h, ncell;  // chunk cell box (cb_w x cb_h cells)
+    int wcol0;              // first column of this grid's cells in the scatter weight rows
+    float inv_cb_w, inv_fp_w;
+};
+
+struct Train16Desc {
+    Grid16 grid[NT_MAX_GRIDS];
+    const float *tex[4]; // reference textures (pitch 4, image size), output rows 4t .. 4t+3
+    int tex_nch[4];
+    float tex_w[4];      // loss weight of texture t's rows
+    int ntex;
+    int image_w, image_h, off_x, off_y, region_w, num_samples;
+    uint32_t step;
+    int tiles_x, nwg, xcd_per; // xcd_per > 0: workgroups of one XCD take consecutive tiles
+    int fp_floats;
+    int group_off, group_bytes, tile_bytes; // per 4-wave group: target tile, then the union
+    int wcols;                              // halves per scatter-weight row (one row per sample)
+    int8_t perm[NT_MAX_OUTPUTS];            // output index of output row r
+    const uint4 *wfrags;
+    const float *wbias;
+    float *partial; // [nwg * groups][grad_total]
+};
+
+struct Prep16Desc {
+    MlpDesc mlp;
+    int8_t perm[NT_MAX_OUTPUTS];
+    uint4 *frags;
+    float *bias;
+};
+
 // Weight-fragment preparation (once per train step) for the train kernel.
 struct PrepDesc {
     MlpDesc mlp;
@@ -179,6 +215,13 @@ size_t train_xt_bytes(int shape);
 size_t train_weight_bytes(int shape);
 size_t train_frag_bytes(int shape);
 hipError_t launch_prep_weights(int shape, const PrepDesc &d, hipStream_t s);
+// 16-channel kernel: groups of four waves per workgroup (1 or 2) for this shape, the
+// static LDS bytes (weights), the transposes' bytes, and the launchers.
+int train16_groups(int shape);
+size_t train16_head_bytes(int shape);
+size_t train16_transpose_bytes(int shape);
+hipError_t launch_prep16(int shape, const Prep16Desc &d, hipStream_t s);
+hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream_t s);
 int train_grad_total(int shape);
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s);
 hipError_t launch_forward(int shape, int mode, const FwdDesc &d, hipStream_t s);

@@ -1,0 +1,658 @@
+// nt_train16.hip — the fused training pass (TrainLoopPass, train.cu:818-915, with
+// mlp.h:101-362 and util/atomic.h) specialised for 16-channel unconstrained latents on
+// gfx950: the path of the 2- and 4-grid networks (32->64->64->16, 64->64->64->64->16).
+//
+// A workgroup is NG groups of four waves (NG = 2 for the 2-grid network: two waves per
+// SIMD, so one wave's LDS and memory latency hides behind the other's work). It owns a
+// 64 x 8NG block of region positions; group gr walks rows [8gr, 8gr + 8) as four 16 x 8
+// chunks of 128 samples, one 32-sample MFMA tile per wave. Per chunk:
+//   - the group's Catmull-Rom target tile is fetched into registers first and written to
+//     its own LDS region after the forward pass, so the loads overlap sampling and MLP;
+//   - lane group g (lane = 32g + c, sample c) gathers grids g and g + 2 only, so each
+//     lane computes one bilinear footprint per fragment pair; the layer-0 weight
+//     fragments carry the matching input-feature order;
+//   - output rows are ordered 4t + channel for reference texture t, so lane group g
+//     evaluates exactly textures g and g + 2 (16 exact Catmull-Rom taps from LDS); the
+//     last layer's weight fragments carry the matching output permutation;
+//   - dW = X^T dY per layer on MFMA over the group's 128 samples from LDS transposes,
+//     each wave owning fixed 32x32 dW tiles accumulated in fp32 registers;
+//   - the latent scatter is an MFMA reduction D[cell][ch] = sum_s W[cell][s] dX0[s][ch]
+//     over the chunk's cell box (fp32 corner weights split into fp16 hi + lo). Each lane
+//     keeps one scatter-weight row per sample and clears only its own entries, and the
+//     rows are read transposed with ds_read_b64_tr_b16. D is added into the workgroup's
+//     footprint box with LDS float adds and flushed once with global float atomics.
+// MLP gradients go to one partial row per group, summed by the deterministic two-stage
+// reduction of nt_train.hip.
+#include "nt_train_parts.hpp"
+
+namespace ntk {
+
+// Layer-0 input feature of element e of k-step fragment q in lane group g: lane group g
+// holds grids g and g + 2, channels 8(q & 1) .. 8(q & 1) + 7.
+__host__ __device__ constexpr int grid_feature(int q, int g, int e)
+{
+    return 16 * (g + 2 * (q >> 1)) + 8 * (q & 1) + e;
+}
+
+constexpr int kTileTexels = kTileW * kTileH;
+
+template <class S, int NG>
+struct T16Layout {
+    static constexpr int G = S::K0 / 16;
+    static constexpr int frag_bytes = S::all_frags() * kWave * 16;
+    static constexpr int bias_bytes = ((S::bias_total() * 4 + 15) / 16) * 16;
+    static constexpr int head_bytes = frag_bytes + bias_bytes;
+    static constexpr int slots = (S::dw_total() + 3) / 4;
+};
+
+// ---- weight preparation ----------------------------------------------------------------
+
+template <class S>
+__device__ h8 weight_fragment16(const MlpDesc &m, const int8_t *perm, int idx)
+{
+    const int f = idx / kWave, lane = idx % kWave, c = lane & 31, g = lane >> 5;
+    h8 v;
+    int l = 0;
+    const bool fwd = f < S::fwd_total();
+    if (fwd) {
+        while (l + 1 < S::L && f >= S::fwd_off(l + 1))
+            ++l;
+    } else {
+        while (l + 1 < S::L && f >= S::bwd_off(l + 1))
+            ++l;
+    }
+    const int kin = S::kin(l), kout = S::kout(l);
+    const bool last = l == S::L - 1;
+    const uint16_t *W = m.W[l];
+    if (fwd) {
+        // Forward fragment (a, q): A[row][kk] = W_l[n][k], row = 32a + c, n = the output of
+        // that row (permuted on the last layer), k = the input of (q, g, e).
+        const int local = f - S::fwd_off(l), qn = kin / 16;
+        const int a = local / qn, q = local % qn;
+        const int row = 32 * a + c;
+        const int n = last ? (row < NT_MAX_OUTPUTS ? perm[row] : kout) : row;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = l == 0 ? grid_feature(q, g, e) : chained_feature(q, g, e);
+            v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+        }
+    } else {
+        // Backward fragment (mt, q): A[k][kk] = W_l[n][k], k = 32mt + c, n = the output of
+        // chained row (q, g, e).
+        const int local = f - S::bwd_off(l), qn = kout / 16;
+        const int mt = local / qn, q = local % qn;
+        const int k = 32 * mt + c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int row = chained_feature(q, g, e);
+            const int n = last ? perm[row] : row;
+            v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+        }
+    }
+    return v;
+}
+
+template <class S>
+__device__ float bias_value16(const MlpDesc &m, const int8_t *perm, int idx)
+{
+    int l = 0;
+    while (l + 1 < S::L && idx >= S::bias_off(l + 1))
+        ++l;
+    int n = idx - S::bias_off(l);
+    if (l == S::L - 1) {
+        if (n >= NT_MAX_OUTPUTS)
+            return 0.f;
+        n = perm[n];
+    }
+    return n < m.sizes[l + 1] ? h2f(m.B[l][n]) : 0.f;
+}
+
+template <class S>
+__global__ __launch_bounds__(256) void prep16_kernel(Prep16Desc d)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < S::all_frags() * kWave)
+        d.frags[i] = __builtin_bit_cast(uint4, weight_fragment16<S>(d.mlp, d.perm, i));
+    if (i < S::bias_total())
+        d.bias[i] = bias_value16<S>(d.mlp, d.perm, i);
+}
+
+// ---- device pieces ---------------------------------------------------------------------
+
+__device__ __forceinline__ h4 lds_read_tr16(const _Float16 *p)
+{
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p);
+    return __builtin_bit_cast(h4, v);
+}
+
+// Start the copy of the chunk's target tile (texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of
+// every texture, wrapped like the reference's texture objects, main.cpp:613-621) into the
+// group's LDS tile with global_load_lds_dwordx4: wave w copies items 64(w + 4k) + lane,
+// each wave instruction filling 64 consecutive float4 slots. No registers are held; the
+// caller waits for vmcnt(0) before the barrier that publishes the tile.
+__device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *tile, int cx0, int cy0,
+                                                 int wave, int lane)
+{
+    const int n = d.ntex * kTileTexels;
+    for (int base = 64 * wave; base < n; base += 64 * 4) {
+        const int i = base + lane;
+        if (i < n) {
+            const int t = i / kTileTexels, rem = i - t * kTileTexels;
+            const int ty = rem / kTileW, tx = rem - ty * kTileW;
+            int gx = cx0 - kTileX0 + tx, gy = cy0 - kTileX0 + ty;
+            gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
+            gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
+            const float *tex = t == 0 ? d.tex[0] : t == 1 ? d.tex[1] : t == 2 ? d.tex[2] : d.tex[3];
+            __builtin_amdgcn_global_load_lds((const void *)(tex + ((int64_t)gy * d.image_w + gx) * 4),
+                                             (__attribute__((address_space(3))) void *)(tile + base), 16, 0, 0);
+        }
+    }
+}
+
+// Catmull-Rom targets and loss weights of the lane's eight output rows 8j + 4g + ch,
+// j = 0, 1: texture t = g + 2j, channel ch (train.cu:105-157; 16 taps, exact weights,
+// the fp32 fma order of the scalar restatement). Rows without a texture channel are the
+// reference's unused outputs: target 0, weight 1.
+__device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float4 *tile, int cx0, int cy0,
+                                               float u, float v, int g, float (&t)[8], float (&wt)[8])
+{
+    float wx[4], wy[4];
+    const int gx0 = cr_axis(u, d.image_w, wx), gy0 = cr_axis(v, d.image_h, wy);
+    const int x0 = gx0 - (cx0 - kTileX0), y0 = gy0 - (cy0 - kTileX0);
+    const bool inside = x0 >= 0 && x0 + 3 < kTileW && y0 >= 0 && y0 + 3 < kTileH;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int ti = g + 2 * j;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (ti < d.ntex) {
+            if (inside) {
+                const float4 *base = tile + ti * kTileTexels + y0 * kTileW + x0;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float4 p = base[jj * kTileW + i];
+                        const float wxy = wx[i] * wy[jj];
+                        acc[0] = fmaf(p.x, wxy, acc[0]);
+                        acc[1] = fmaf(p.y, wxy, acc[1]);
+                        acc[2] = fmaf(p.z, wxy, acc[2]);
+                        acc[3] = fmaf(p.w, wxy, acc[3]);
+                    }
+            } else {
+                const float *tex = ti == 0 ? d.tex[0] : ti == 1 ? d.tex[1] : ti == 2 ? d.tex[2] : d.tex[3];
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int y = wrap_coord(gy0 + jj, d.image_h);
+                    for (int i = 0; i < 4; ++i) {
+                        const int x = wrap_coord(gx0 + i, d.image_w);
+                        const float4 p = *(const float4 *)(tex + ((int64_t)y * d.image_w + x) * 4);
+                        const float wxy = wx[i] * wy[jj];
+                        acc[0] = fmaf(p.x, wxy, acc[0]);
+                        acc[1] = fmaf(p.y, wxy, acc[1]);
+                        acc[2] = fmaf(p.z, wxy, acc[2]);
+                        acc[3] = fmaf(p.w, wxy, acc[3]);
+                    }
+                }
+            }
+        }
+        const int nch = ti < d.ntex ? (ti == 0 ? d.tex_nch[0] : ti == 1 ? d.tex_nch[1] : ti == 2 ? d.tex_nch[2] : d.tex_nch[3]) : 0;
+        const float lw = ti == 0 ? d.tex_w[0] : ti == 1 ? d.tex_w[1] : ti == 2 ? d.tex_w[2] : d.tex_w[3];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            t[4 * j + r] = r < nch ? acc[r] : 0.f;
+            wt[4 * j + r] = r < nch ? lw : 1.f;
+        }
+    }
+}
+
+// Bilinear footprint of grid gi at mip 0 (train.cu:284-303, z = 0).
+__device__ __forceinline__ Footprint footprint16(const Grid16 &gr, float u, float v)
+{
+    return bilinear_footprint(u, v, gr.w, gr.h, 1.f);
+}
+
+// Gather grids g + 2j of the lane into fragments 2j (channels 0-7) and 2j + 1 (8-15);
+// corner contributions rounded to fp16 and summed in fp16, corner by corner
+// (train.cu:293-310).
+template <int G>
+__device__ __forceinline__ void gather16(const Train16Desc &d, float u, float v, int g, h8 (&x)[G])
+{
+#pragma unroll
+    for (int j = 0; j < G / 2; ++j) {
+        const Grid16 &ga = d.grid[2 * j], &gb = d.grid[2 * j + 1];
+        const float *vals = g ? gb.values : ga.values;
+        const int w = g ? gb.w : ga.w, h = g ? gb.h : ga.h;
+        const Footprint f = bilinear_footprint(u, v, w, h, 1.f);
+        h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int tx = wrap_near(f.x0 + (c & 1), w), ty = wrap_near(f.y0 + (c >> 1), h);
+            const float4 *p = (const float4 *)(vals + ((int64_t)ty * w + tx) * 16);
+            const float4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+            lo = accumulate_products(lo, f.w[c], a0, a1);
+            hi = accumulate_products(hi, f.w[c], a2, a3);
+        }
+        x[2 * j] = lo;
+        x[2 * j + 1] = hi;
+    }
+}
+
+// Write the layer-0 inputs transposed, rows in natural feature order.
+template <int G>
+__device__ __forceinline__ void store_inputs_transposed(_Float16 *buf, const h8 (&v)[G], int col, int g)
+{
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            buf[grid_feature(q, g, e) * kRowStride + col] = v[q][e];
+}
+
+// ---- the kernel ----------------------------------------------------------------------------
+
+template <class S, int NG>
+__global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc d)
+{
+    using LY = T16Layout<S, NG>;
+    constexpr int G = LY::G, L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
+    static_assert(KQ0 == G && (G == 2 || G == 4), "one 16-channel grid per k-step pair");
+    extern __shared__ __align__(16) unsigned char smem[];
+    h8 *frags = (h8 *)smem;
+    float *bias = (float *)(smem + LY::frag_bytes);
+    float *fp = (float *)(smem + LY::head_bytes);
+
+    const int tid = threadIdx.x, t256 = tid & (kTrainThreads - 1), gr = tid >> 8;
+    const int lane = tid & 63, wave = t256 >> 6, c = lane & 31, g = lane >> 5;
+    unsigned char *gbase = smem + d.group_off + gr * d.group_bytes;
+    float4 *tile = (float4 *)gbase;
+    _Float16 *un = (_Float16 *)(gbase + d.tile_bytes);
+    _Float16 *xt = un;
+    _Float16 *dyt = xt + TrainLayout<S>::xt_rows * kRowStride;
+    _Float16 *dxt = un;                       // scatter: dX0^T [K0][kRowStride]
+    _Float16 *whi = un + S::K0 * kRowStride;  // scatter weights [sample][wcols], hi
+    _Float16 *wlo = whi + kChunk * d.wcols;   // ... lo
+
+    {
+        const uint4 *src = d.wfrags;
+        uint4 *dst = (uint4 *)frags;
+        for (int i = tid; i < S::all_frags() * kWave; i += kTrainThreads * NG)
+            dst[i] = src[i];
+        for (int i = tid; i < S::bias_total(); i += kTrainThreads * NG)
+            bias[i] = d.wbias[i];
+        float4 *f4 = (float4 *)fp;
+        for (int i = tid; i < d.fp_floats / 4; i += kTrainThreads * NG)
+            f4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    int b = blockIdx.x;
+    if (d.xcd_per > 0)
+        b = (b & 7) * d.xcd_per + (b >> 3); // the workgroups of one XCD share an L2: give them neighbouring tiles
+    const int tx0 = (b % d.tiles_x) * (kChunkW * 4), ty0 = (b / d.tiles_x) * (kChunkH * NG);
+    // Footprint box origin per grid: the lowest texel any sample of the workgroup can touch.
+    int flo_x[G], flo_y[G];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        const Grid16 &q = d.grid[gi];
+        flo_x[gi] = (int)floorf((float)(d.off_x + tx0) * (float)q.w / (float)d.image_w - 0.5f) - 1;
+        flo_y[gi] = (int)floorf((float)(d.off_y + ty0) * (float)q.h / (float)d.image_h - 0.5f) - 1;
+    }
+
+    f16v dwacc[LY::slots];
+#pragma unroll
+    for (int j = 0; j < LY::slots; ++j)
+        dwacc[j] = (f16v)0.f;
+    float dbacc[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+        dbacc[l] = 0.f;
+
+    const int col = 32 * wave + c; // this lane's sample column in the group's transposes
+    for (int chunk = 0; chunk < 4; ++chunk) {
+        const int cx0 = d.off_x + tx0 + chunk * kChunkW, cy0 = d.off_y + ty0 + kChunkH * gr;
+        tile_fetch_async(d, tile, cx0, cy0, wave, lane);
+
+        // ---- sample position (train.cu:827-844)
+        const int sx = tx0 + chunk * kChunkW + (c & 15);
+        const int sy = ty0 + kChunkH * gr + 2 * wave + (c >> 4);
+        const uint32_t sidx = (uint32_t)sy * (uint32_t)d.region_w + (uint32_t)sx;
+        const bool valid = sx < d.region_w && sidx < (uint32_t)d.num_samples;
+        uint32_t st = mix_seed(sidx, d.step);
+        const float jx = uniform01(st) - 0.5f;
+        const float jy = uniform01(st) - 0.5f;
+        const float px = clampf((float)(uint32_t)(d.off_x + sx) + 0.5f + jx, 0.5f, (float)d.image_w - 0.5f);
+        const float py = clampf((float)(uint32_t)(d.off_y + sy) + 0.5f + jy, 0.5f, (float)d.image_h - 0.5f);
+        const float u = px / (float)d.image_w;
+        const float v = py / (float)d.image_h;
+
+        h8 x0[KQ0];
+        if (valid) {
+            gather16<G>(d, u, v, g, x0);
+        } else {
+#pragma unroll
+            for (int q = 0; q < KQ0; ++q)
+                x0[q] = (h8)(_Float16)0.f;
+        }
+
+        // ---- forward (mlp.h:65-99)
+        h8 xh[NH][HQ];
+        {
+            f16v acc[HA];
+            layer_forward<KQ0, HA>(frags + S::fwd_off(0) * kWave, bias + S::bias_off(0), x0, acc, lane);
+            to_fragments<HQ, HA, true>(acc, xh[0]);
+#pragma unroll
+            for (int l = 1; l < NH; ++l) {
+                layer_forward<HQ, HA>(frags + S::fwd_off(l) * kWave, bias + S::bias_off(l), xh[l - 1], acc, lane);
+                to_fragments<HQ, HA, true>(acc, xh[l]);
+            }
+        }
+        f16v out[1];
+        layer_forward<HQ, 1>(frags + S::fwd_off(L - 1) * kWave, bias + S::bias_off(L - 1), xh[NH - 1], out, lane);
+
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads(); // target tile staged
+
+        // ---- targets and loss gradient (train.cu:105-157, 876-888): dL/dy = fp16(2 w (y - t) / N)
+        h8 dyo[1];
+        {
+            float tgt[8], tw[8];
+            lane_targets16(d, tile, cx0, cy0, u, v, g, tgt, tw);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float y = (float)(_Float16)out[0][e];
+                const float err = y - tgt[e];
+                const float grd = 2.f * tw[e] * err / (float)d.num_samples;
+                dyo[0][e] = valid ? (_Float16)grd : (_Float16)0.f;
+            }
+        }
+
+        // ---- backward, last layer (mlp.h:302-362)
+        h8 dyh[HQ];
+        store_transposed<1, true>(dyt, dyo, col, g);
+        store_transposed<HQ, true>(xt, xh[NH - 1], col, g);
+        {
+            f16v acc[HA];
+            layer_backward_dx<1, HA>(frags + S::bwd_off(L - 1) * kWave, dyo, acc, lane);
+#pragma unroll
+            for (int q = 0; q < HQ; ++q)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    dyh[q][e] = xh[NH - 1][q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e]
+                                                                : (_Float16)0.f;
+        }
+        __syncthreads();
+        dw_phase<S, L - 1>(xt, dyt, dwacc, dbacc[L - 1], wave, lane, t256);
+        __syncthreads();
+
+        // ---- hidden layers L-2 .. 1
+        backward_hidden<S, L - 2>(xt, dyt, frags, xh, dyh, dwacc, dbacc, col, wave, lane, t256);
+
+        // ---- first layer: dW with the gathered inputs, dX = latent gradient
+        store_transposed<HQ, true>(dyt, dyh, col, g);
+        store_inputs_transposed<G>(xt, x0, col, g);
+        h8 dx0[KQ0];
+        {
+            constexpr int MA = S::t32(S::K0);
+            f16v acc[MA];
+            layer_backward_dx<HQ, MA>(frags + S::bwd_off(0) * kWave, dyh, acc, lane);
+#pragma unroll
+            for (int q = 0; q < KQ0; ++q) {
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const f2 pv = {acc[q >> 1][8 * (q & 1) + e], acc[q >> 1][8 * (q & 1) + e + 1]};
+                    const h2 hv = __builtin_convertvector(pv, h2);
+                    dx0[q][e] = hv[0];
+                    dx0[q][e + 1] = hv[1];
+                }
+            }
+        }
+        __syncthreads();
+        dw_phase<S, 0>(xt, dyt, dwacc, dbacc[0], wave, lane, t256);
+        __syncthreads();
+
+        // ---- latent scatter (train.cu:460-509) as an MFMA reduction over the chunk
+        // Part 1: dX0^T, this sample's weight row (own entries cleared first), and corners
+        // outside the chunk cell box straight into the footprint box.
+        store_transposed<KQ0, true>(dxt, dx0, col, g);
+        {
+            _Float16 *rhi = whi + col * d.wcols, *rlo = wlo + col * d.wcols;
+            const float ru = rn32(u), rv = rn32(v);
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                const Grid16 &q = d.grid[gi];
+                const int bx = (int)floorf((float)cx0 * (float)q.w / (float)d.image_w - 0.5f);
+                const int by = (int)floorf((float)cy0 * (float)q.h / (float)d.image_h - 0.5f);
+                const Footprint f = footprint16(q, ru, rv);
+                if ((gi & 1) == g) { // lane group g owns grids g, g + 2 of the weight row
+                    uint4 *zh = (uint4 *)(rhi + q.wcol0), *zl = (uint4 *)(rlo + q.wcol0);
+                    for (int k = 0; k < (q.ncell + 15) / 16 * 2; ++k) {
+                        zh[k] = make_uint4(0u, 0u, 0u, 0u);
+                        zl[k] = make_uint4(0u, 0u, 0u, 0u);
+                    }
+                }
+#pragma unroll
+                for (int corner = 0; corner < 4; ++corner) {
+                    const int tx = f.x0 + (corner & 1), ty = f.y0 + (corner >> 1);
+                    const int cx = tx - bx, cy = ty - by;
+                    const float w = f.w[corner];
+                    if (cx >= 0 && cx < q.cb_w && cy >= 0 && cy < q.cb_h) {
+                        if (valid && (gi & 1) == g) {
+                            const int k = q.wcol0 + cy * q.cb_w + cx;
+                            const _Float16 hi = (_Float16)w;
+                            rhi[k] = hi;
+                            rlo[k] = (_Float16)(w - (float)hi);
+                        }
+                    } else if (valid) {
+                        // This lane's dX0 channels of grid gi are rows chained(gi, g, e).
+                        const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
+                        const bool inbox = lx >= 0 && lx < q.fp_w && ly >= 0 && ly < q.fp_h;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int ch = chained_feature(0, g, e);
+                            const float val = w * (float)dx0[gi][e];
+                            if (inbox)
+                                lds_add(fp + q.fp_off + (ly * q.fp_w + lx) * 16 + ch, val);
+                            else
+                                global_add(q.grads + ((int64_t)wrap_near(ty, q.h) * q.w + wrap_near(tx, q.w)) * 16 + ch, val);
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // Part 2: one task per (grid, 16-cell tile), dealt to the group's waves.
+        {
+            int task = 0;
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                const Grid16 &q = d.grid[gi];
+                const int bx = (int)floorf((float)cx0 * (float)q.w / (float)d.image_w - 0.5f);
+                const int by = (int)floorf((float)cy0 * (float)q.h / (float)d.image_h - 0.5f);
+                const int ntile = (q.ncell + 15) >> 4;
+                for (int t = 0; t < ntile; ++t, ++task) {
+                    if ((task & 3) != wave)
+                        continue;
+                    const int i16 = lane & 15, grp = lane >> 4;
+                    const _Float16 *bp = dxt + (gi * 16 + i16) * kRowStride + 8 * grp;
+                    const int acol = q.wcol0 + 16 * t + 4 * (i16 & 3);
+                    f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kk = 0; kk < kChunk / 32; ++kk) {
+                        const int arow = 32 * kk + 8 * grp + (i16 >> 2);
+                        const h8 bv = *(const h8 *)(bp + 32 * kk);
+                        const h4 h0 = lds_read_tr16(whi + arow * d.wcols + acol);
+                        const h4 h1 = lds_read_tr16(whi + (arow + 4) * d.wcols + acol);
+                        const h4 l0 = lds_read_tr16(wlo + arow * d.wcols + acol);
+                        const h4 l1 = lds_read_tr16(wlo + (arow + 4) * d.wcols + acol);
+                        acc = mfma16(__builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7), bv, acc);
+                        acc = mfma16(__builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7), bv, acc);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int cell = 16 * t + 4 * grp + r;
+                        if (cell >= q.ncell || acc[r] == 0.f)
+                            continue;
+                        const int cy = (int)(((float)cell + 0.5f) * q.inv_cb_w);
+                        const int cxx = cell - cy * q.cb_w;
+                        const int tx = bx + cxx, ty = by + cy;
+                        const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
+                        if (lx >= 0 && lx < q.fp_w && ly >= 0 && ly < q.fp_h)
+                            lds_add(fp + q.fp_off + (ly * q.fp_w + lx) * 16 + i16, acc[r]);
+                        else
+                            global_add(q.grads + ((int64_t)wrap_near(ty, q.h) * q.w + wrap_near(tx, q.w)) * 16 + i16, acc[r]);
+                    }
+                }
+            }
+        }
+        // The next chunk writes the union only after its first barrier.
+    }
+
+    __syncthreads();
+    // ---- flush the footprint box with global float atomics
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        const Grid16 &q = d.grid[gi];
+        const float4 *box = (const float4 *)(fp + q.fp_off);
+        const int n4 = q.fp_w * q.fp_h * 4;
+        for (int i = tid; i < n4; i += kTrainThreads * NG) {
+            const float4 val = box[i];
+            if (val.x == 0.f && val.y == 0.f && val.z == 0.f && val.w == 0.f)
+                continue;
+            const int cell = i >> 2, part = i & 3;
+            const int ly = (int)(((float)cell + 0.5f) * q.inv_fp_w), lx = cell - ly * q.fp_w;
+            const int gx = wrap_near(flo_x[gi] + lx, q.w), gy = wrap_near(flo_y[gi] + ly, q.h);
+            float *dst = q.grads + ((int64_t)gy * q.w + gx) * 16 + 4 * part;
+            if (val.x != 0.f)
+                global_add(dst, val.x);
+            if (val.y != 0.f)
+                global_add(dst + 1, val.y);
+            if (val.z != 0.f)
+                global_add(dst + 2, val.z);
+            if (val.w != 0.f)
+                global_add(dst + 3, val.w);
+        }
+    }
+
+    // ---- per-group MLP gradient partial (output rows of the last layer un-permuted)
+    float *part = d.partial + ((int64_t)blockIdx.x * NG + gr) * S::grad_total();
+#pragma unroll
+    for (int j = 0; j < LY::slots; ++j) {
+        const int t = 4 * j + wave;
+        if (t < S::dw_total()) {
+            int l = 0;
+#pragma unroll
+            for (int k = 0; k < L; ++k)
+                if (t >= S::dw_start(k) && t < S::dw_start(k) + S::dw_tiles(k))
+                    l = k;
+            int kin = S::kin(0), kout = S::kout(0), start = S::dw_start(0), off = S::grad_off(0);
+#pragma unroll
+            for (int k = 1; k < L; ++k)
+                if (l == k) {
+                    kin = S::kin(k);
+                    kout = S::kout(k);
+                    start = S::dw_start(k);
+                    off = S::grad_off(k);
+                }
+            const int kb = (kin + 31) / 32;
+            const int a = (t - start) / kb, bb = (t - start) % kb;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = 32 * a + 8 * (e >> 2) + 4 * g + (e & 3);
+                const int k = 32 * bb + c;
+                if (row < kout && k < kin) {
+                    const int n = l == L - 1 ? d.perm[row] : row;
+                    part[off + n * kin + k] = dwacc[j][e];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+        if (t256 < 4 * S::kout(l) && (t256 & 3) == 0) {
+            const int row = t256 >> 2;
+            const int n = l == L - 1 ? d.perm[row] : row;
+            part[S::grad_off(l) + S::kout(l) * S::kin(l) + n] = dbacc[l];
+        }
+}
+
+// ---- launchers ---------------------------------------------------------------------------
+
+using ShapeC2 = Shape<32, 64, 2>;
+using ShapeC4 = Shape<64, 64, 3>;
+
+template <class S, int NG>
+static hipError_t launch16(const Train16Desc &d, size_t lds, hipStream_t s)
+{
+    auto k = train16_kernel<S, NG>;
+    static size_t configured = 0;
+    if (lds > 65536 && lds > configured) {
+        hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        configured = lds;
+    }
+    hipLaunchKernelGGL(k, dim3(d.nwg), dim3(kTrainThreads * NG), lds, s, d);
+    return hipGetLastError();
+}
+
+int train16_groups(int shape)
+{
+    return shape == kShapeC2 ? 2 : shape == kShapeC4 ? 1 : 0;
+}
+
+size_t train16_head_bytes(int shape)
+{
+    switch (shape) {
+    case kShapeC2:
+        return T16Layout<ShapeC2, 2>::head_bytes;
+    case kShapeC4:
+        return T16Layout<ShapeC4, 1>::head_bytes;
+    default:
+        return 0;
+    }
+}
+
+size_t train16_transpose_bytes(int shape)
+{
+    switch (shape) {
+    case kShapeC2:
+        return TrainLayout<ShapeC2>::transpose_bytes;
+    case kShapeC4:
+        return TrainLayout<ShapeC4>::transpose_bytes;
+    default:
+        return 0;
+    }
+}
+
+template <class S>
+static hipError_t prep16(const Prep16Desc &d, hipStream_t s)
+{
+    const int n = S::all_frags() * kWave > S::bias_total() ? S::all_frags() * kWave : S::bias_total();
+    hipLaunchKernelGGL(prep16_kernel<S>, dim3((n + 255) / 256), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_prep16(int shape, const Prep16Desc &d, hipStream_t s)
+{
+    switch (shape) {
+    case kShapeC2:
+        return prep16<ShapeC2>(d, s);
+    case kShapeC4:
+        return prep16<ShapeC4>(d, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream_t s)
+{
+    switch (shape) {
+    case kShapeC2:
+        return launch16<ShapeC2, 2>(d, lds, s);
+    case kShapeC4:
+        return launch16<ShapeC4, 1>(d, lds, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+} // namespace ntk
