@@ -343,6 +343,8 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         wcols += 16 * ((q.ncell + 15) / 16);
         q.inv_cb_w = 1.f / (float)q.cb_w;
         q.inv_fp_w = 1.f / (float)q.fp_w;
+        q.rx = (float)g.width / (float)p->image_width;
+        q.ry = (float)g.height / (float)p->image_height;
         if (!aligned16(q.values) || !aligned16(q.grads))
             return;
     }
@@ -354,6 +356,10 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     un = scatter > un ? scatter : un;
     d.tile_bytes = d.ntex * kTileW * kTileH * 16;
     d.group_bytes = (int)((d.tile_bytes + un + 15) & ~(size_t)15);
+    // The second group's region carries its dW accumulators to the first at the end.
+    const size_t handoff = ((size_t)train16_slots(plan->shape) * 16 + (size_t)p->mlp.num_layers) * kTrainThreads * 4;
+    if (NG == 2 && (size_t)d.group_bytes < handoff)
+        return;
     d.group_off = (int)((head + (size_t)fp * 4 + 15) & ~(size_t)15);
     const size_t lds = (size_t)d.group_off + (size_t)NG * d.group_bytes;
     if (lds > kMaxLds)
@@ -362,7 +368,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->groups = NG;
     plan->lds = lds;
     plan->nwg = d.nwg;
-    plan->rows = d.nwg * NG;
+    plan->rows = d.nwg; // the groups of a workgroup merge their partials in LDS
     plan->stage1_blocks = (plan->rows + plan->rows_per_block - 1) / plan->rows_per_block;
     plan->workspace = plan->weight_bytes +
                       ((size_t)plan->rows + (size_t)plan->stage1_blocks) * (size_t)plan->P * sizeof(float);

@@ -52,11 +52,24 @@ __device__ __forceinline__ h8 accumulate_products(h8 acc, float w, float4 a, flo
                                          5, 6, 7);
     return acc + q;
 }
-// The same for eight fp16 values (each widened to fp32 exactly before the product).
+// The same for eight fp16 values. The product is formed as fma(w, v, +0) so that it maps
+// to one v_fma_mix_f32 (fp16 operand widened exactly): the same fp32 value as w * v except
+// that an exact zero is +0, which changes no sum, since the fp16 accumulator starting at
+// +0 under round-to-nearest can never become -0.
 __device__ __forceinline__ h8 accumulate_products(h8 acc, float w, h8 v)
 {
-    return accumulate_products(acc, w, make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]),
-                               make_float4((float)v[4], (float)v[5], (float)v[6], (float)v[7]));
+    f2 p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        p[i][0] = rn32(fmaf(w, (float)v[2 * i], 0.f));
+        p[i][1] = rn32(fmaf(w, (float)v[2 * i + 1], 0.f));
+    }
+    const h2 q0 = __builtin_convertvector(p[0], h2), q1 = __builtin_convertvector(p[1], h2);
+    const h2 q2 = __builtin_convertvector(p[2], h2), q3 = __builtin_convertvector(p[3], h2);
+    const h8 q = __builtin_shufflevector(__builtin_shufflevector(q0, q1, 0, 1, 2, 3),
+                                         __builtin_shufflevector(q2, q3, 0, 1, 2, 3), 0, 1, 2, 3, 4,
+                                         5, 6, 7);
+    return acc + q;
 }
 
 __device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }

@@ -79,6 +79,7 @@ struct Grid16 {
     int cb_w, cb_h, ncell;  // chunk cell box (cb_w x cb_h cells)
     int wcol0;              // first column of this grid's cells in the scatter weight rows
     float inv_cb_w, inv_fp_w;
+    float rx, ry; // grid texels per image texel
 };
 
 struct Train16Desc {
@@ -96,7 +97,7 @@ struct Train16Desc {
     int8_t perm[NT_MAX_OUTPUTS];            // output index of output row r
     const uint4 *wfrags;
     const float *wbias;
-    float *partial; // [nwg * groups][grad_total]
+    float *partial; // [nwg][grad_total]
 };
 
 struct Prep16Desc {
@@ -220,6 +221,7 @@ hipError_t launch_prep_weights(int shape, const PrepDesc &d, hipStream_t s);
 int train16_groups(int shape);
 size_t train16_head_bytes(int shape);
 size_t train16_transpose_bytes(int shape);
+int train16_slots(int shape); // dW tiles per wave
 hipError_t launch_prep16(int shape, const Prep16Desc &d, hipStream_t s);
 hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream_t s);
 int train_grad_total(int shape);

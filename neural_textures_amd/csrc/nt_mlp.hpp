@@ -194,6 +194,17 @@ __device__ __forceinline__ void to_fragments(const f16v (&acc)[NA], h8 (&y)[NQ])
     }
 }
 
+// ReLU backward (mlp.h:240-252): dY_prev = fp16(acc) where the layer input x > 0, else 0.
+template <int NQ, int NA>
+__device__ __forceinline__ void relu_backward(const f16v (&acc)[NA], const h8 (&x)[NQ], h8 (&dy)[NQ])
+{
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            dy[q][e] = x[q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e] : (_Float16)0.f;
+}
+
 // dX for one layer: acc[m] = W dY over the layer's output features (chained dY frags).
 template <int NQ, int MA>
 __device__ __forceinline__ void layer_backward_dx(const h8 *frags, const h8 (&dy)[NQ],

@@ -758,12 +758,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
         {
             f16v acc[HA];
             layer_backward_dx<1, HA>(frags + S::bwd_off(L - 1) * kWave, dyo, acc, lane);
-#pragma unroll
-            for (int q = 0; q < HQ; ++q)
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    dyh[q][e] = xh[NH - 1][q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e]
-                                                                : (_Float16)0.f;
+            relu_backward<HQ, HA>(acc, xh[NH - 1], dyh);
         }
         __syncthreads();
         dw_phase<S, L - 1>(xt, dyt, dwacc, dbacc[L - 1], wave, lane, tid);

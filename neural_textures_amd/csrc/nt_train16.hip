@@ -126,26 +126,43 @@ __device__ __forceinline__ h4 lds_read_tr16(const _Float16 *p)
     return __builtin_bit_cast(h4, v);
 }
 
+// Uniform copies of descriptor fields: selecting between two of them per lane then stays
+// a register select instead of a per-lane load from the kernel-argument segment.
+__device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float sreg(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+template <class T>
+__device__ __forceinline__ T *sreg(T *p)
+{
+    const uint64_t u = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (T *)(((uint64_t)hi << 32) | lo);
+}
+
 // Start the copy of the chunk's target tile (texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of
 // every texture, wrapped like the reference's texture objects, main.cpp:613-621) into the
-// group's LDS tile with global_load_lds_dwordx4: wave w copies items 64(w + 4k) + lane,
-// each wave instruction filling 64 consecutive float4 slots. No registers are held; the
-// caller waits for vmcnt(0) before the barrier that publishes the tile.
+// group's LDS tile with global_load_lds_dwordx4: per texture, wave w copies texels
+// 64(w + 4k) + lane, each wave instruction filling 64 consecutive float4 slots. No
+// registers are held; the caller waits for vmcnt(0) before the barrier that publishes it.
 __device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *tile, int cx0, int cy0,
                                                  int wave, int lane)
 {
-    const int n = d.ntex * kTileTexels;
-    for (int base = 64 * wave; base < n; base += 64 * 4) {
-        const int i = base + lane;
-        if (i < n) {
-            const int t = i / kTileTexels, rem = i - t * kTileTexels;
-            const int ty = rem / kTileW, tx = rem - ty * kTileW;
-            int gx = cx0 - kTileX0 + tx, gy = cy0 - kTileX0 + ty;
-            gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
-            gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
-            const float *tex = t == 0 ? d.tex[0] : t == 1 ? d.tex[1] : t == 2 ? d.tex[2] : d.tex[3];
-            __builtin_amdgcn_global_load_lds((const void *)(tex + ((int64_t)gy * d.image_w + gx) * 4),
-                                             (__attribute__((address_space(3))) void *)(tile + base), 16, 0, 0);
+    for (int t = 0; t < d.ntex; ++t) {
+        const float *tex = d.tex[t];
+        float4 *dst = tile + t * kTileTexels;
+        for (int base = 64 * wave; base < kTileTexels; base += 64 * 4) {
+            const int i = base + lane;
+            if (i < kTileTexels) {
+                const int ty = i / kTileW, tx = i - ty * kTileW;
+                int gx = cx0 - kTileX0 + tx, gy = cy0 - kTileX0 + ty;
+                gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
+                gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
+                __builtin_amdgcn_global_load_lds((const void *)(tex + ((int64_t)gy * d.image_w + gx) * 4),
+                                                 (__attribute__((address_space(3))) void *)(dst + base), 16, 0, 0);
+            }
         }
     }
 }
@@ -180,7 +197,7 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
                         acc[3] = fmaf(p.w, wxy, acc[3]);
                     }
             } else {
-                const float *tex = ti == 0 ? d.tex[0] : ti == 1 ? d.tex[1] : ti == 2 ? d.tex[2] : d.tex[3];
+                const float *tex = g ? sreg(d.tex[2 * j + 1]) : sreg(d.tex[2 * j]);
                 for (int jj = 0; jj < 4; ++jj) {
                     const int y = wrap_coord(gy0 + jj, d.image_h);
                     for (int i = 0; i < 4; ++i) {
@@ -195,8 +212,8 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
                 }
             }
         }
-        const int nch = ti < d.ntex ? (ti == 0 ? d.tex_nch[0] : ti == 1 ? d.tex_nch[1] : ti == 2 ? d.tex_nch[2] : d.tex_nch[3]) : 0;
-        const float lw = ti == 0 ? d.tex_w[0] : ti == 1 ? d.tex_w[1] : ti == 2 ? d.tex_w[2] : d.tex_w[3];
+        const int nch = ti < d.ntex ? (g ? sreg(d.tex_nch[2 * j + 1]) : sreg(d.tex_nch[2 * j])) : 0;
+        const float lw = g ? sreg(d.tex_w[2 * j + 1]) : sreg(d.tex_w[2 * j]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             t[4 * j + r] = r < nch ? acc[r] : 0.f;
@@ -220,17 +237,23 @@ __device__ __forceinline__ void gather16(const Train16Desc &d, float u, float v,
 #pragma unroll
     for (int j = 0; j < G / 2; ++j) {
         const Grid16 &ga = d.grid[2 * j], &gb = d.grid[2 * j + 1];
-        const float *vals = g ? gb.values : ga.values;
-        const int w = g ? gb.w : ga.w, h = g ? gb.h : ga.h;
+        const float *vals = g ? sreg(gb.values) : sreg(ga.values);
+        const int w = g ? sreg(gb.w) : sreg(ga.w), h = g ? sreg(gb.h) : sreg(ga.h);
         const Footprint f = bilinear_footprint(u, v, w, h, 1.f);
-        h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
+        float4 t[4][4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int tx = wrap_near(f.x0 + (c & 1), w), ty = wrap_near(f.y0 + (c >> 1), h);
             const float4 *p = (const float4 *)(vals + ((int64_t)ty * w + tx) * 16);
-            const float4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
-            lo = accumulate_products(lo, f.w[c], a0, a1);
-            hi = accumulate_products(hi, f.w[c], a2, a3);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                t[c][k] = p[k];
+        }
+        h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            lo = accumulate_products(lo, f.w[c], t[c][0], t[c][1]);
+            hi = accumulate_products(hi, f.w[c], t[c][2], t[c][3]);
         }
         x[2 * j] = lo;
         x[2 * j + 1] = hi;
@@ -372,12 +395,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         {
             f16v acc[HA];
             layer_backward_dx<1, HA>(frags + S::bwd_off(L - 1) * kWave, dyo, acc, lane);
-#pragma unroll
-            for (int q = 0; q < HQ; ++q)
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    dyh[q][e] = xh[NH - 1][q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e]
-                                                                : (_Float16)0.f;
+            relu_backward<HQ, HA>(acc, xh[NH - 1], dyh);
         }
         __syncthreads();
         dw_phase<S, L - 1>(xt, dyt, dwacc, dbacc[L - 1], wave, lane, t256);
@@ -419,8 +437,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 const Grid16 &q = d.grid[gi];
-                const int bx = (int)floorf((float)cx0 * (float)q.w / (float)d.image_w - 0.5f);
-                const int by = (int)floorf((float)cy0 * (float)q.h / (float)d.image_h - 0.5f);
+                const int bx = (int)floorf(fmaf((float)cx0, q.rx, -0.5f));
+                const int by = (int)floorf(fmaf((float)cy0, q.ry, -0.5f));
                 const Footprint f = footprint16(q, ru, rv);
                 if ((gi & 1) == g) { // lane group g owns grids g, g + 2 of the weight row
                     uint4 *zh = (uint4 *)(rhi + q.wcol0), *zl = (uint4 *)(rlo + q.wcol0);
@@ -465,8 +483,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 const Grid16 &q = d.grid[gi];
-                const int bx = (int)floorf((float)cx0 * (float)q.w / (float)d.image_w - 0.5f);
-                const int by = (int)floorf((float)cy0 * (float)q.h / (float)d.image_h - 0.5f);
+                const int bx = (int)floorf(fmaf((float)cx0, q.rx, -0.5f));
+                const int by = (int)floorf(fmaf((float)cy0, q.ry, -0.5f));
                 const int ntile = (q.ncell + 15) >> 4;
                 for (int t = 0; t < ntile; ++t, ++task) {
                     if ((task & 3) != wave)
@@ -532,8 +550,33 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         }
     }
 
-    // ---- per-group MLP gradient partial (output rows of the last layer un-permuted)
-    float *part = d.partial + ((int64_t)blockIdx.x * NG + gr) * S::grad_total();
+    // ---- the workgroup's MLP gradient partial (output rows of the last layer un-permuted):
+    // group 1 hands its accumulators to group 0 through its own (now idle) LDS region.
+    if constexpr (NG == 2) {
+        float *xch = (float *)(smem + d.group_off + d.group_bytes);
+        if (gr == 1) {
+#pragma unroll
+            for (int j = 0; j < LY::slots; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    xch[(j * 16 + e) * kTrainThreads + t256] = dwacc[j][e];
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+                xch[(LY::slots * 16 + l) * kTrainThreads + t256] = dbacc[l];
+        }
+        __syncthreads();
+        if (gr == 1)
+            return;
+#pragma unroll
+        for (int j = 0; j < LY::slots; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                dwacc[j][e] += xch[(j * 16 + e) * kTrainThreads + t256];
+#pragma unroll
+        for (int l = 0; l < L; ++l)
+            dbacc[l] += xch[(LY::slots * 16 + l) * kTrainThreads + t256];
+    }
+    float *part = d.partial + (int64_t)blockIdx.x * S::grad_total();
 #pragma unroll
     for (int j = 0; j < LY::slots; ++j) {
         const int t = 4 * j + wave;
@@ -606,6 +649,18 @@ size_t train16_head_bytes(int shape)
         return T16Layout<ShapeC2, 2>::head_bytes;
     case kShapeC4:
         return T16Layout<ShapeC4, 1>::head_bytes;
+    default:
+        return 0;
+    }
+}
+
+int train16_slots(int shape)
+{
+    switch (shape) {
+    case kShapeC2:
+        return T16Layout<ShapeC2, 2>::slots;
+    case kShapeC4:
+        return T16Layout<ShapeC4, 1>::slots;
     default:
         return 0;
     }

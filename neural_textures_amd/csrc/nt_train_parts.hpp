@@ -76,13 +76,17 @@ __device__ __forceinline__ void dw_phase(const _Float16 *xt, const _Float16 *dyt
     if (tid < 4 * kout) {
         const int n = tid >> 2, part = tid & 3;
         const h8 *row = (const h8 *)(dyt + n * kRowStride + 32 * part);
+        // fp32 sum of 32 fp16 values, two per v_dot2_f32_f16 (exact products by one).
+        const h2 one = {(_Float16)1.f, (_Float16)1.f};
         float s = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const h8 r = row[k];
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                s += (float)r[e];
+            for (int e = 0; e < 8; e += 2) {
+                const h2 pair = {r[e], r[e + 1]};
+                s = __builtin_amdgcn_fdot2(pair, one, s, false);
+            }
         }
         s += __shfl_xor(s, 1);
         s += __shfl_xor(s, 2);
@@ -114,12 +118,7 @@ __device__ __forceinline__ void backward_hidden(_Float16 *xt, _Float16 *dyt, con
         store_transposed<HQ, true>(xt, xh[l - 1], col, g);
         f16v acc[HA];
         layer_backward_dx<HQ, HA>(frags + S::bwd_off(l) * kWave, dyh, acc, lane);
-#pragma unroll
-        for (int q = 0; q < HQ; ++q)
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                dyh[q][e] = xh[l - 1][q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e]
-                                                           : (_Float16)0.f;
+        relu_backward<HQ, HA>(acc, xh[l - 1], dyh);
         __syncthreads();
         dw_phase<S, l>(xt, dyt, dwacc, dbacc[l], wave, lane, tid);
         __syncthreads();
