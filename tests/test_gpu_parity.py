@@ -134,6 +134,8 @@ TRAIN_CASES = [
     ("ref", 128, (64, 32), (100, 110), abi.NT_UNCONSTRAINED),  # region wraps past the edge
     ("c2", 128, (64, 32), (16, 40), abi.NT_UNCONSTRAINED),
     ("c2", 64, (50, 21), (3, 5), abi.NT_UNCONSTRAINED),         # ragged region and tail row
+    ("c2", 128, (64, 48), (100, 90), abi.NT_UNCONSTRAINED),     # wraps: clamped edge samples
+    ("c4", 128, (64, 32), (96, 120), abi.NT_UNCONSTRAINED),
     ("c4", 128, (64, 32), (8, 8), abi.NT_UNCONSTRAINED),
     ("ref", 64, (32, 16), (0, 0), abi.NT_BLOCK_FEATURES),
     ("ref", 64, (32, 16), (5, 7), abi.NT_FINALIZE),
