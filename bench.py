@@ -34,10 +34,11 @@ PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 FLOP_PER_TRAIN_SAMPLE_C2 = 40320   # 3 x 2 x (32*64 + 64*64 + 64*9)
 FLOP_PER_DECODE_PIXEL = 26112      # 2 x (64*64*3 + 64*12)
+FLOP_PER_TRAIN_SAMPLE_C4 = 78336   # 3 x 2 x (64*64*3 + 64*12)
 # HBM bytes per config-2 train-kernel launch: rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000,
 # the factors being what the two counters read for a 256 MiB device copy (--copy-probe).
 # Counters cannot be read live; re-measure whenever the train kernel changes.
-TRAIN_HBM_BYTES_PER_LAUNCH = (9075.4 * 2.0 + 18664.0) * 1024
+TRAIN_HBM_BYTES_PER_LAUNCH = (8168.4 * 2.0 + 16192.1) * 1024
 
 
 def log(msg):
@@ -71,27 +72,48 @@ class HipEvents:
         self.hip.hipEventDestroy(e)
 
 
-def build_config2(device, seed=1337):
-    """BASELINE config 2 on the device."""
+# Train configurations: image size, target channels (packed per texture), latent grids
+# (size, mips), MLP sizes, training region side (batch = region^2).
+TRAIN_CONFIGS = {
+    2: dict(image=2048, channels=9, per_texture=3, grids=[(512, 8), (256, 7)],
+            mlp=[32, 64, 64, 9], region=512),
+    4: dict(image=4096, channels=12, per_texture=4, grids=[(1024, 9), (512, 8), (256, 7), (128, 6)],
+            mlp=[64, 64, 64, 64, 12], region=1024),
+}
+
+
+def build_config(device, cfg=2, seed=1337):
+    """A BASELINE train configuration on the device (synthetic target, U[-1,1] latents)."""
     from neural_textures_amd import params as P, synthetic as S
 
-    textures = S.target_textures(2048, 2048, 9, 3, seed, device)
-    grids = [S.latent_grid(512, 512, 8, 16, seed + 1, device),
-             S.latent_grid(256, 256, 7, 16, seed + 2, device)]
-    net = P.make_network([32, 64, 64, 9], used_outputs=9, rng=np.random.default_rng(seed),
+    c = TRAIN_CONFIGS[cfg]
+    n = c["image"]
+    textures = S.target_textures(n, n, c["channels"], c["per_texture"], seed, device)
+    grids = [S.latent_grid(size, size, mips, 16, seed + 1 + i, device)
+             for i, (size, mips) in enumerate(c["grids"])]
+    net = P.make_network(c["mlp"], used_outputs=c["mlp"][-1], rng=np.random.default_rng(seed),
                          init="xavier").converted(True, device)
-    return P.TrainState(grids, net, textures, 2048, 2048, 512 * 512, region_width=512,
+    r = c["region"]
+    return P.TrainState(grids, net, textures, n, n, r * r, region_width=r,
                         network_adam=(0.9, 0.999, 5e-3, 1e-8),
                         feature_adam=(0.9, 0.999, 1e-2, 1e-8))
 
 
-def bench_train(lib, nt, args, ev):
+def build_config2(device, seed=1337):
+    """BASELINE config 2 on the device."""
+    return build_config(device, 2, seed)
+
+
+def bench_train(lib, nt, args, ev, cfg=2, steps=None, warmup=None):
     import torch
 
     from neural_textures_amd import abi
 
     device = "cuda:0"
-    st = build_config2(device)
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
+    st = build_config(device, cfg)
+    image, region = st.image_width, st.region_width
     p = st.params()
     ws_bytes = lib.nt_train_workspace_bytes(C.byref(p), abi.NT_UNCONSTRAINED)
     assert ws_bytes > 0, lib.nt_last_error().decode()
@@ -99,9 +121,9 @@ def bench_train(lib, nt, args, ev):
     p = st.params()
     stream = torch.cuda.current_stream()
     sh = C.c_void_p(stream.cuda_stream)
-    total = args.warmup + args.steps
+    total = warmup + steps
     rng = np.random.default_rng(20260411)  # region offsets, like main.cpp:1033-1044
-    offs = rng.integers(0, 2048 - 512 + 1, size=(total + args.steps, 2))
+    offs = rng.integers(0, image - region + 1, size=(total + steps, 2))
     base_lr = 1e-2
     torch.cuda.synchronize()
 
@@ -115,19 +137,19 @@ def bench_train(lib, nt, args, ev):
         nt.check(lib.nt_optimize_network(C.byref(p), sh))
         nt.check(lib.nt_optimize_latents(C.byref(p), abi.NT_UNCONSTRAINED, sh))
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.warmup, total):
+    for i in range(warmup, total):
         step(i)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    ms_per_step = (t1 - t0) * 1e3 / steps
 
     # Dominant kernel (the fused train kernel) timed with events on its own stream.
-    pairs = [(ev.create(), ev.create()) for _ in range(args.steps)]
-    for k in range(args.steps):
+    pairs = [(ev.create(), ev.create()) for _ in range(steps)]
+    for k in range(steps):
         step(total + k, pairs[k])
     torch.cuda.synchronize()
     kms = [ev.ms(a, b) for a, b in pairs]
@@ -268,13 +290,14 @@ def cpu_baseline(st_gpu, budget_s=12.0):
     O.ntref_optimize_latents(C.byref(p), 0)
     t_adam = time.perf_counter() - t
     per_step = t_train / n * 262144 + t_adam
+    nlat = sum(g.texels * g.channels for g in host.grids)
     return {
         "value": 262144 / per_step,
         "unit": "train texels/s",
         "cores": 1,
         "kind": "port",
         "sample": f"{n} of 262,144 samples of one config-2 step (train {t_train:.2f} s) + one "
-                  f"dense lazy-Adam pass over all 5.6M latent and 7K network parameters "
+                  f"dense lazy-Adam pass over all {nlat / 1e6:.1f}M latent and 7K network parameters "
                   f"({t_adam:.2f} s), extrapolated to a full step; scalar C oracle, -O2, "
                   f"one thread, host {os.uname().nodename}",
     }
@@ -338,7 +361,7 @@ def main():
             "step": "nt_train_step + nt_optimize_network + nt_optimize_latents",
         },
         "roofline": {
-            "kernel": "train_kernel<Shape<32,64,2>,16,UNCONSTRAINED> (fused sample/target/MLP fwd+bwd/scatter)",
+            "kernel": "train16_kernel<Shape<32,64,2>,2> (fused sample/target/MLP fwd+bwd/scatter)",
             "bound": "mfma",
             "achieved": achieved,
             "peak": PEAK_FP16_TFLOPS,
@@ -352,6 +375,19 @@ def main():
         },
     }
     if not args.no_extras:
+        log("bench: config 4 train steps")
+        st4, ms4, k4, _ = bench_train(lib, nt, args, ev, cfg=4, steps=10, warmup=3)
+        n4 = st4.num_samples
+        ach4 = FLOP_PER_TRAIN_SAMPLE_C4 * n4 / (k4 / 1e3) / 1e12
+        result["train_config4"] = {
+            "value": n4 / (ms4 / 1e3), "unit": "texels/s", "ms_per_step": ms4, "steps": 10,
+            "workload": "BASELINE config 4 train step: 1,048,576 jittered samples of a 1024^2 region "
+                        "of a 4096^2x12 target; latents 16ch@1024^2..128^2 (4 grids); MLP "
+                        "64-64-64-64-12 fp16; lazy Adam",
+            "roofline": {"kernel": "train16_kernel<Shape<64,64,3>,1>", "bound": "mfma",
+                         "achieved": ach4, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": ach4 / PEAK_FP16_TFLOPS, "launch_ms_mean": k4}}
+        del st4
         log("bench: config 5 decode")
         dms, kms, npx, wsb = bench_decode(lib, nt, ev)
         dach = FLOP_PER_DECODE_PIXEL * npx / (kms / 1e3) / 1e12
