@@ -1023,6 +1023,9 @@ int nt_decode(const nt_decode_params *p, void *stream)
         d.cgrid[gi].w = g.width;
         d.cgrid[gi].h = g.height;
         d.cgrid[gi].num_mips = g.num_mips;
+        d.grid[gi].w = g.width;
+        d.grid[gi].h = g.height;
+        d.grid[gi].num_mips = g.num_mips;
         for (int m = 0; m < NT_MAX_MIPS; ++m)
             d.cgrid[gi].byte_off[m] = g.byte_offset[m];
     }

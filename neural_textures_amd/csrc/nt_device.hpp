@@ -72,6 +72,22 @@ __device__ __forceinline__ h8 accumulate_products(h8 acc, float w, h8 v)
     return acc + q;
 }
 
+// Uniform copies of descriptor fields: selecting between two of them per lane then stays
+// a register select instead of a per-lane load from the kernel-argument segment.
+__device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float sreg(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+template <class T>
+__device__ __forceinline__ T *sreg(T *p)
+{
+    const uint64_t u = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (T *)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)bits_h(b); }

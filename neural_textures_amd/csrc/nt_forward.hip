@@ -183,36 +183,90 @@ __device__ __forceinline__ void sample_codec(const FwdDesc &d, float u, float v,
     }
 }
 
-// Trilinear sample of the expanded fp16 texels (16 channels per grid; lane group g takes
-// channels 8g .. 8g+7 of every grid). The texel values are the codec's decoded fp16
-// numbers, so the result equals sample_codec's bit for bit.
-template <int KQ>
-__device__ __forceinline__ void sample_half16(const FwdDesc &d, float u, float v, float z, int g,
-                                              h8 (&x)[KQ])
+// ---- decode (16 channels per grid) ---------------------------------------------------
+// Lane group g samples grids g and g + 2 (all 16 channels; the layer-0 weights are staged in
+// grid_feature order), so each lane evaluates one footprint per grid and mip. A corner
+// contribution is accumulated as one fp16 fma per channel, weight rounded to fp16
+// (v_pk_fma_f16, two channels per instruction): within an fp16 rounding of the training
+// path's fp32-product-then-round accumulation, which decode does not need to reproduce.
+// Mip offsets come from a per-workgroup LDS table (the mip index differs per pixel).
+
+__device__ __forceinline__ void fma_corner16(h8 &lo, h8 &hi, float w, h8 vlo, h8 vhi)
+{
+    const h8 w8 = (h8)(_Float16)w;
+    lo = __builtin_elementwise_fma(w8, vlo, lo);
+    hi = __builtin_elementwise_fma(w8, vhi, hi);
+}
+
+// The sixteen decoded fp16 channels of texel (tx, ty) of one codec mip level.
+__device__ __forceinline__ void codec_texel16(const uint8_t *base, int bw, int tx, int ty, h8 &lo, h8 &hi)
+{
+    const uint8_t *rec = base + ((int64_t)(ty >> 2) * bw + (tx >> 2)) * (12 * 16);
+    const int pix = ((ty & 3) << 2) + (tx & 3);
+    const uint4 e0 = *(const uint4 *)rec, e1 = *(const uint4 *)(rec + 16);
+    const uint4 e2 = *(const uint4 *)(rec + 32), e3 = *(const uint4 *)(rec + 48);
+    const uint2 ix = *(const uint2 *)(rec + 64 + pix * 8);
+    const uint32_t ends[16] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w,
+                               e2.x, e2.y, e2.z, e2.w, e3.x, e3.y, e3.z, e3.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        lo[e] = bits_h((uint16_t)codec_unkey(codec_interp(ends[e] & 0xFFFFu, ends[e] >> 16, (ix.x >> (4 * e)) & 15)));
+        hi[e] = bits_h((uint16_t)codec_unkey(
+            codec_interp(ends[8 + e] & 0xFFFFu, ends[8 + e] >> 16, (ix.y >> (4 * e)) & 15)));
+    }
+}
+
+// EXPANDED: sample the fp16 texels of the first decode pass; else decode the blocks.
+template <int G, bool EXPANDED>
+__device__ __forceinline__ void sample_decode16(const FwdDesc &d, const int64_t *mip_tab, float u, float v,
+                                                float z, int g, h8 (&x)[G])
 {
 #pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-        h8 acc = (h8)(_Float16)0.f;
-        if (q < d.G) {
-            const GridDesc &gr = d.grid[q];
-            int mips[2];
-            float mw[2];
-            const int nm = mip_pair(gr.num_mips, z, mips, mw);
-            for (int mi = 0; mi < nm; ++mi) {
-                const int w = mip_dim(gr.w, mips[mi]), h = mip_dim(gr.h, mips[mi]);
-                const Footprint f = bilinear_footprint(u, v, w, h, mw[mi]);
-                const uint4 *base = (const uint4 *)(d.half_values[q] + gr.mip_off[mips[mi]] * 16) + g;
-                const int x0 = wrap_edge(f.x0, w), x1 = wrap_edge(f.x0 + 1, w);
-                const int r0 = wrap_edge(f.y0, h) * w, r1 = wrap_edge(f.y0 + 1, h) * w;
-                const uint4 t0 = base[2 * (r0 + x0)], t1 = base[2 * (r0 + x1)];
-                const uint4 t2 = base[2 * (r1 + x0)], t3 = base[2 * (r1 + x1)];
-                acc = accumulate_products(acc, f.w[0], __builtin_bit_cast(h8, t0));
-                acc = accumulate_products(acc, f.w[1], __builtin_bit_cast(h8, t1));
-                acc = accumulate_products(acc, f.w[2], __builtin_bit_cast(h8, t2));
-                acc = accumulate_products(acc, f.w[3], __builtin_bit_cast(h8, t3));
+    for (int j = 0; j < G / 2; ++j) {
+        const int gi = 2 * j + g;
+        const GridDesc &ga = d.grid[2 * j], &gb = d.grid[2 * j + 1];
+        const int gw = g ? sreg(gb.w) : sreg(ga.w), gh = g ? sreg(gb.h) : sreg(ga.h);
+        const int nmips = g ? sreg(gb.num_mips) : sreg(ga.num_mips);
+        const uint16_t *hv = g ? sreg(d.half_values[2 * j + 1]) : sreg(d.half_values[2 * j]);
+        const uint8_t *blocks = g ? sreg(d.cgrid[2 * j + 1].blocks) : sreg(d.cgrid[2 * j].blocks);
+        int mips[2];
+        float mw[2];
+        const int nm = mip_pair(nmips, z, mips, mw);
+        h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
+        for (int mi = 0; mi < nm; ++mi) {
+            const int w = mip_dim(gw, mips[mi]), h = mip_dim(gh, mips[mi]);
+            const Footprint f = bilinear_footprint(u, v, w, h, mw[mi]);
+            const int x0 = wrap_edge(f.x0, w), x1 = wrap_edge(f.x0 + 1, w);
+            const int y0 = wrap_edge(f.y0, h), y1 = wrap_edge(f.y0 + 1, h);
+            const int64_t off = mip_tab[gi * NT_MAX_MIPS + mips[mi]];
+            h8 v0l, v0h, v1l, v1h, v2l, v2h, v3l, v3h;
+            if constexpr (EXPANDED) {
+                const uint4 *t = (const uint4 *)(hv + off * 16);
+                const uint4 a0 = t[2 * (y0 * w + x0)], a1 = t[2 * (y0 * w + x0) + 1];
+                const uint4 b0 = t[2 * (y0 * w + x1)], b1 = t[2 * (y0 * w + x1) + 1];
+                const uint4 c0 = t[2 * (y1 * w + x0)], c1 = t[2 * (y1 * w + x0) + 1];
+                const uint4 e0 = t[2 * (y1 * w + x1)], e1 = t[2 * (y1 * w + x1) + 1];
+                v0l = __builtin_bit_cast(h8, a0), v0h = __builtin_bit_cast(h8, a1);
+                v1l = __builtin_bit_cast(h8, b0), v1h = __builtin_bit_cast(h8, b1);
+                v2l = __builtin_bit_cast(h8, c0), v2h = __builtin_bit_cast(h8, c1);
+                v3l = __builtin_bit_cast(h8, e0), v3h = __builtin_bit_cast(h8, e1);
+            } else {
+                const uint8_t *base = blocks + off;
+                const int bw = (w + 3) >> 2;
+                codec_texel16(base, bw, x0, y0, v0l, v0h);
+                codec_texel16(base, bw, x1, y0, v1l, v1h);
+                codec_texel16(base, bw, x0, y1, v2l, v2h);
+                codec_texel16(base, bw, x1, y1, v3l, v3h);
             }
+            fma_corner16(lo, hi, f.w[0], v0l, v0h);
+            fma_corner16(lo, hi, f.w[1], v1l, v1h);
+            fma_corner16(lo, hi, f.w[2], v2l, v2h);
+            fma_corner16(lo, hi, f.w[3], v3l, v3h);
+            // One mip level's eight 16-byte loads at a time keeps the wave within 128 VGPRs.
+            __builtin_amdgcn_sched_barrier(0);
         }
-        x[q] = acc;
+        x[2 * j] = lo;
+        x[2 * j + 1] = hi;
     }
 }
 
@@ -230,7 +284,16 @@ __global__ __launch_bounds__(kFwdThreads, fwd_min_blocks<MODE>()) void forward_k
     h8 *frags = (h8 *)smem;
     float *bias = (float *)(smem + LY::bias_off);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
-    stage_weights<S, true>(d.mlp, frags, bias, tid, kFwdThreads);
+    constexpr bool kDecode16 = (MODE == kFwdDecode || MODE == kFwdDecode16) && C == 16;
+    __shared__ int64_t mip_tab[kDecode16 ? NT_MAX_GRIDS * NT_MAX_MIPS : 1];
+    stage_weights<S, true, kDecode16>(d.mlp, frags, bias, tid, kFwdThreads);
+    if constexpr (kDecode16) {
+        // Texel (expanded pass) or byte (blocks) offset of every (grid, mip) level.
+        if (tid < NT_MAX_GRIDS * NT_MAX_MIPS) {
+            const int gi = tid / NT_MAX_MIPS, m = tid % NT_MAX_MIPS;
+            mip_tab[tid] = gi < d.G ? (MODE == kFwdDecode16 ? d.grid[gi].mip_off[m] : d.cgrid[gi].byte_off[m]) : 0;
+        }
+    }
     __syncthreads();
 
     float sse = 0.f;
@@ -277,8 +340,8 @@ __global__ __launch_bounds__(kFwdThreads, fwd_min_blocks<MODE>()) void forward_k
             u = posx / (float)d.image_w;
             v = posy / (float)d.image_h;
             const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
-            if constexpr (MODE == kFwdDecode16)
-                sample_half16<KQ0>(d, u, v, z, g, x0);
+            if constexpr (kDecode16)
+                sample_decode16<KQ0, MODE == kFwdDecode16>(d, mip_tab, u, v, z, g, x0);
             else
                 sample_codec<C, KQ0>(d, u, v, z, g, x0);
         }

@@ -81,6 +81,13 @@ __device__ __forceinline__ int chained_feature(int q, int g, int e)
     return 16 * q + 8 * (e >> 2) + 4 * g + (e & 3);
 }
 __device__ __forceinline__ int natural_feature(int q, int g, int e) { return 16 * q + 8 * g + e; }
+// Layer-0 input feature of element e of k-step fragment q in lane group g: lane group g
+// holds grids g and g + 2, channels 8(q & 1) .. 8(q & 1) + 7.
+__host__ __device__ constexpr int grid_feature(int q, int g, int e)
+{
+    return 16 * (g + 2 * (q >> 1)) + 8 * (q & 1) + e;
+}
+
 
 // Network pointers and unpadded sizes, as kernels see them.
 struct MlpDesc {
@@ -92,7 +99,7 @@ struct MlpDesc {
 
 // Element idx = fragment * 64 + lane of the forward/backward weight fragments, in the
 // order layer_forward / layer_backward_dx read them.
-template <class S>
+template <class S, bool GRID_ORDER = false>
 __device__ h8 weight_fragment(const MlpDesc &m, int idx)
 {
     const int f = idx / kWave, lane = idx % kWave, c = lane & 31, g = lane >> 5;
@@ -116,7 +123,7 @@ __device__ h8 weight_fragment(const MlpDesc &m, int idx)
         const int n = 32 * a + c;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int k = l == 0 ? natural_feature(q, g, e) : chained_feature(q, g, e);
+            const int k = l > 0 ? chained_feature(q, g, e) : GRID_ORDER ? grid_feature(q, g, e) : natural_feature(q, g, e);
             v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
         }
     } else {
@@ -145,14 +152,15 @@ __device__ float bias_value(const MlpDesc &m, int idx)
     return n < m.sizes[l + 1] ? h2f(m.B[l][n]) : 0.f;
 }
 
-// Stage forward (and, unless FWD_ONLY, backward) weight fragments and fp32 biases in LDS.
-// All threads of the block take part; the caller synchronises afterwards.
-template <class S, bool FWD_ONLY = false>
+// Stage forward (and, unless FWD_ONLY, backward) weight fragments and fp32 biases in LDS,
+// layer 0 in natural or grid_feature input order. All threads of the block take part; the
+// caller synchronises afterwards.
+template <class S, bool FWD_ONLY = false, bool GRID_ORDER = false>
 __device__ void stage_weights(const MlpDesc &m, h8 *frags, float *bias, int tid, int nthreads)
 {
     constexpr int nfrags = FWD_ONLY ? S::fwd_total() : S::all_frags();
     for (int idx = tid; idx < nfrags * kWave; idx += nthreads)
-        frags[idx] = weight_fragment<S>(m, idx);
+        frags[idx] = weight_fragment<S, GRID_ORDER>(m, idx);
     for (int idx = tid; idx < S::bias_total(); idx += nthreads)
         bias[idx] = bias_value<S>(m, idx);
 }

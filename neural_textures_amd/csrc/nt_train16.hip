@@ -27,13 +27,6 @@
 
 namespace ntk {
 
-// Layer-0 input feature of element e of k-step fragment q in lane group g: lane group g
-// holds grids g and g + 2, channels 8(q & 1) .. 8(q & 1) + 7.
-__host__ __device__ constexpr int grid_feature(int q, int g, int e)
-{
-    return 16 * (g + 2 * (q >> 1)) + 8 * (q & 1) + e;
-}
-
 constexpr int kTileTexels = kTileW * kTileH;
 
 template <class S, int NG>
@@ -124,22 +117,6 @@ __device__ __forceinline__ h4 lds_read_tr16(const _Float16 *p)
     typedef short s4 __attribute__((ext_vector_type(4)));
     const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p);
     return __builtin_bit_cast(h4, v);
-}
-
-// Uniform copies of descriptor fields: selecting between two of them per lane then stays
-// a register select instead of a per-lane load from the kernel-argument segment.
-__device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ float sreg(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
-}
-template <class T>
-__device__ __forceinline__ T *sreg(T *p)
-{
-    const uint64_t u = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-    return (T *)(((uint64_t)hi << 32) | lo);
 }
 
 // Start the copy of the chunk's target tile (texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of
