@@ -58,7 +58,8 @@ typedef enum nt_status {
     NT_ERR_MISALIGNED = 3,       /* a buffer is not aligned as documented */
     NT_ERR_UNSUPPORTED = 4,      /* valid, but no kernel is built for this shape */
     NT_ERR_WORKSPACE = 5,        /* workspace missing or smaller than required */
-    NT_ERR_HIP = 6               /* the HIP runtime reported an error (launch) */
+    NT_ERR_HIP = 6,              /* the HIP runtime reported an error (launch) */
+    NT_ERR_FORMAT = 7            /* a model image fails its checks (nt_model_load) */
 } nt_status;
 
 /* Mirrors TrainingKernelType (train.h:22-27). */
@@ -198,7 +199,8 @@ const char *nt_last_error(void);
 int64_t nt_mip_chain_layout(int width, int height, int num_mips, int64_t *mip_offset);
 /* The same for 4x4 block storage (blocks per dimension = max(size>>2, 1), train.cu:220). */
 int64_t nt_block_chain_layout(int width, int height, int num_mips, int64_t *block_offset);
-/* Bytes of scratch nt_train_step needs for these parameters (0 on error). */
+/* Bytes of scratch nt_train_step needs for these parameters (0 on error); also enough for
+ * nt_inference's fixed-order SSE. */
 size_t nt_train_workspace_bytes(const nt_params *params, nt_kernel_type type);
 
 /* Profiling hook (no reference counterpart): the next nt_train_step, nt_optimize_latents,
@@ -225,8 +227,14 @@ int nt_optimize_network(const nt_params *params, void *stream);
 int nt_optimize_latents(const nt_params *params, nt_kernel_type type, void *stream);
 
 /* Full-image inference at texel centres, mip 0 (InvokeInference, train.cu:1050-1062 ->
- * :917-961): writes inference_output and adds the squared error to inference_mse_accum. */
+ * :917-961): writes inference_output and adds the squared error to inference_mse_accum.
+ * With params->workspace of at least nt_inference_workspace_bytes (every train workspace
+ * of the same params is), the squared errors are summed in a fixed order, so the SSE is
+ * the same bits on every run; without one, partial sums are added atomically in arrival
+ * order, as the reference does (train.cu:960). */
 int nt_inference(const nt_params *params, void *stream);
+/* Workspace bytes for the fixed-order SSE of nt_inference (0 on a bad argument). */
+size_t nt_inference_workspace_bytes(const nt_params *params);
 
 /*
  * Tiny-MLP forward on given fp16 inputs (the ForwardPass* functions of mlp.h:18-99, as
@@ -302,6 +310,71 @@ size_t nt_decode_workspace_bytes(const nt_decode_params *params);
  * trilinear sample of every grid, MLP forward, fp16 output.
  */
 int nt_decode(const nt_decode_params *params, void *stream);
+
+/* ---- model container ----------------------------------------------------------------
+ *
+ * A versioned, checksummed file image of a neural texture (no reference counterpart: the
+ * reference writes only PNG renders, main.cpp:855-904). It always holds the fp16 network;
+ * with NT_MODEL_CODEC the codec-quantized latent mip chains (what nt_decode reads), and
+ * with NT_MODEL_STATE the training state (fp32 unconstrained latents, their Adam moments,
+ * the network's Adam moments and the step) so a training run resumes from it. Host memory
+ * only; moving buffers to and from the device is the caller's.
+ *
+ * Image (little-endian): a 64-byte header {"NTMODEL\0", version, header bytes, section
+ * count, contents, image bytes, crc32 of the description and the section table}, the
+ * description (32 int32: the fields of nt_model_info in order, zero padded), a table of
+ * 32-byte section entries {type, index, offset, bytes, crc32}, then the sections, each at
+ * a 256-byte aligned offset. A reader accepts images of its version only and checks every
+ * size and checksum.
+ */
+#define NT_MODEL_VERSION 1
+#define NT_MODEL_CODEC 1u /* codec mip chains */
+#define NT_MODEL_STATE 2u /* training state */
+
+typedef struct nt_model_info {
+    uint32_t contents; /* NT_MODEL_CODEC | NT_MODEL_STATE (at least one) */
+    int num_grids;     /* 1..NT_MAX_GRIDS */
+    int channels;      /* per grid: 1..16; 4, 8, 12 or 16 with NT_MODEL_CODEC */
+    int width[NT_MAX_GRIDS];
+    int height[NT_MAX_GRIDS];
+    int num_mips[NT_MAX_GRIDS]; /* 1..NT_MAX_MIPS */
+    int num_layers;             /* network as nt_mlp: 1..NT_MAX_LAYERS */
+    int sizes[NT_MAX_LAYERS + 1]; /* 1..1024 */
+    int used_outputs;             /* 1..sizes[num_layers] */
+    int step;                     /* Adam step of the training state (0 without it) */
+} nt_model_info;
+
+/*
+ * Host buffers of one model, in the layouts of nt_mlp and nt_grid:
+ *   codec[g]       grid g's codec mip chain, nt_codec_mip_chain_layout bytes (CODEC)
+ *   weights[l]     fp16 bits, AlignUp(sizes[l],16) x AlignUp(sizes[l+1],16)
+ *   biases[l]      fp16 bits, sizes[l+1]
+ *   latents[g], latent_moment1[g], latent_moment2[g]   fp32 [texel][channels] over grid
+ *                  g's mips back to back (mip m after the texels of mips < m) (STATE)
+ *   weight_moment1/2[l], bias_moment1/2[l]   fp32, as weights / biases (STATE)
+ * nt_model_load points these into the image (zero copy) and sets absent ones to NULL.
+ */
+typedef struct nt_model_data {
+    const void *codec[NT_MAX_GRIDS];
+    const uint16_t *weights[NT_MAX_LAYERS];
+    const uint16_t *biases[NT_MAX_LAYERS];
+    const float *latents[NT_MAX_GRIDS];
+    const float *latent_moment1[NT_MAX_GRIDS];
+    const float *latent_moment2[NT_MAX_GRIDS];
+    const float *weight_moment1[NT_MAX_LAYERS];
+    const float *weight_moment2[NT_MAX_LAYERS];
+    const float *bias_moment1[NT_MAX_LAYERS];
+    const float *bias_moment2[NT_MAX_LAYERS];
+} nt_model_data;
+
+/* Bytes of the image of a model (0 on a bad description, reason in nt_last_error). */
+size_t nt_model_bytes(const nt_model_info *info);
+/* Writes the image into out (16-byte aligned, out_bytes >= nt_model_bytes). */
+int nt_model_save(const nt_model_info *info, const nt_model_data *data, void *out,
+                  size_t out_bytes);
+/* Checks an image (magic, version, description, table, checksums; in 16-byte aligned) and
+ * fills info and data, whose pointers point into in. NT_ERR_FORMAT if the checks fail. */
+int nt_model_load(const void *in, size_t in_bytes, nt_model_info *info, nt_model_data *data);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,12 @@ NT_ERR_MISALIGNED = 3
 NT_ERR_UNSUPPORTED = 4
 NT_ERR_WORKSPACE = 5
 NT_ERR_HIP = 6
+NT_ERR_FORMAT = 7
+
+# model container
+NT_MODEL_VERSION = 1
+NT_MODEL_CODEC = 1
+NT_MODEL_STATE = 2
 
 # nt_kernel_type (TrainingKernelType, train.h:22-27)
 NT_UNCONSTRAINED = 0
@@ -115,6 +121,30 @@ class nt_decode_params(C.Structure):
     ]
 
 
+class nt_model_info(C.Structure):
+    _fields_ = [
+        ("contents", C.c_uint32), ("num_grids", C.c_int), ("channels", C.c_int),
+        ("width", C.c_int * NT_MAX_GRIDS), ("height", C.c_int * NT_MAX_GRIDS),
+        ("num_mips", C.c_int * NT_MAX_GRIDS),
+        ("num_layers", C.c_int), ("sizes", C.c_int * (NT_MAX_LAYERS + 1)),
+        ("used_outputs", C.c_int), ("step", C.c_int),
+    ]
+
+
+class nt_model_data(C.Structure):
+    _fields_ = [
+        ("codec", C.c_void_p * NT_MAX_GRIDS),
+        ("weights", C.c_void_p * NT_MAX_LAYERS), ("biases", C.c_void_p * NT_MAX_LAYERS),
+        ("latents", C.c_void_p * NT_MAX_GRIDS),
+        ("latent_moment1", C.c_void_p * NT_MAX_GRIDS),
+        ("latent_moment2", C.c_void_p * NT_MAX_GRIDS),
+        ("weight_moment1", C.c_void_p * NT_MAX_LAYERS),
+        ("weight_moment2", C.c_void_p * NT_MAX_LAYERS),
+        ("bias_moment1", C.c_void_p * NT_MAX_LAYERS),
+        ("bias_moment2", C.c_void_p * NT_MAX_LAYERS),
+    ]
+
+
 # Entry points of include/nt/nt.h: name -> (restype, argtypes)
 P = C.POINTER
 SIGNATURES = {
@@ -129,6 +159,7 @@ SIGNATURES = {
     "nt_optimize_network": (C.c_int, [P(nt_params), C.c_void_p]),
     "nt_optimize_latents": (C.c_int, [P(nt_params), C.c_int, C.c_void_p]),
     "nt_inference": (C.c_int, [P(nt_params), C.c_void_p]),
+    "nt_inference_workspace_bytes": (C.c_size_t, [P(nt_params)]),
     "nt_mlp_forward": (C.c_int, [P(nt_mlp), C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
     "nt_forward": (C.c_int, [P(nt_latents), P(nt_mlp), C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                              C.c_void_p, C.c_void_p]),
@@ -138,6 +169,9 @@ SIGNATURES = {
     "nt_codec_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "nt_decode_workspace_bytes": (C.c_size_t, [P(nt_decode_params)]),
     "nt_decode": (C.c_int, [P(nt_decode_params), C.c_void_p]),
+    "nt_model_bytes": (C.c_size_t, [P(nt_model_info)]),
+    "nt_model_save": (C.c_int, [P(nt_model_info), P(nt_model_data), C.c_void_p, C.c_size_t]),
+    "nt_model_load": (C.c_int, [C.c_void_p, C.c_size_t, P(nt_model_info), P(nt_model_data)]),
 }
 
 

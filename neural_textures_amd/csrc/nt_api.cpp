@@ -503,6 +503,17 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
 
 } // namespace
 
+int ntk::report(int status, const char *fmt, ...)
+{
+    if (status == NT_OK)
+        return ok();
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
 extern "C" {
 
 int nt_abi_version(void) { return NT_ABI_VERSION; }
@@ -524,6 +535,8 @@ const char *nt_status_string(int status)
         return "workspace too small";
     case NT_ERR_HIP:
         return "HIP runtime error";
+    case NT_ERR_FORMAT:
+        return "bad model image";
     default:
         return "unknown status";
     }
@@ -571,7 +584,8 @@ size_t nt_train_workspace_bytes(const nt_params *params, nt_kernel_type type)
     TrainPlan plan;
     if (plan_train(params, type, &plan) != NT_OK)
         return 0;
-    return plan.workspace;
+    // Large enough for nt_inference's fixed-order SSE partials too.
+    return std::max(plan.workspace, nt_inference_workspace_bytes(params));
 }
 
 int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
@@ -857,8 +871,28 @@ int nt_inference(const nt_params *p, void *stream)
     d.out32 = p->inference_output;
     d.sse = p->inference_mse_accum;
     d.out_stride = p->mlp.sizes[p->mlp.num_layers];
-    ProfileScope prof((hipStream_t)stream);
-    return hip_status(launch_forward(shape, kFwdInference, d, (hipStream_t)stream), "inference launch");
+    const int partials = forward_blocks(d.count) * kFwdWaves;
+    if (p->workspace && p->workspace_bytes >= (size_t)partials * sizeof(float)) {
+        if (!aligned16(p->workspace))
+            return fail(NT_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+        d.sse_partial = (float *)p->workspace;
+    }
+    hipError_t e;
+    {
+        ProfileScope prof((hipStream_t)stream);
+        e = launch_forward(shape, kFwdInference, d, (hipStream_t)stream);
+    }
+    if (e == hipSuccess && d.sse_partial)
+        e = launch_sse_reduce(d.sse_partial, partials, d.sse, (hipStream_t)stream);
+    return hip_status(e, "inference launch");
+}
+
+size_t nt_inference_workspace_bytes(const nt_params *p)
+{
+    if (!p || p->image_width < 1 || p->image_height < 1 ||
+        (int64_t)p->image_width * p->image_height > (1ll << 31) - 64)
+        return 0;
+    return (size_t)forward_blocks(p->image_width * p->image_height) * kFwdWaves * sizeof(float);
 }
 
 int nt_mlp_forward(const nt_mlp *mlp, const uint16_t *inputs, uint16_t *outputs, int count, void *stream)

@@ -10,7 +10,6 @@
 
 namespace ntk {
 
-constexpr int kFwdThreads = 256;
 
 template <class S>
 struct FwdLayout {
@@ -456,20 +455,45 @@ __global__ __launch_bounds__(kFwdThreads, fwd_min_blocks<MODE>()) void forward_k
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1)
             sse += __shfl_xor(sse, off);
-        if (lane == 0 && sse != 0.f)
-            global_add(d.sse, sse);
+        if (lane == 0) {
+            if (d.sse_partial)
+                d.sse_partial[blockIdx.x * kFwdWaves + wave] = sse;
+            else if (sse != 0.f)
+                global_add(d.sse, sse);
+        }
     }
+}
+
+// The fixed-order SSE reduction: thread t sums partial[t], partial[t + 256], ... in index
+// order, then a pairwise tree over the 256 sums; the result is the same bits on every run.
+__global__ __launch_bounds__(256) void sse_reduce_kernel(const float *partial, int n, float *sse)
+{
+    __shared__ float part[256];
+    const int t = threadIdx.x;
+    float s = 0.f;
+    for (int i = t; i < n; i += 256)
+        s += partial[i];
+    part[t] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w)
+            part[t] += part[t + w];
+        __syncthreads();
+    }
+    if (t == 0)
+        sse[0] = sse[0] + part[0];
+}
+
+hipError_t launch_sse_reduce(const float *partial, int n, float *sse, hipStream_t s)
+{
+    hipLaunchKernelGGL(sse_reduce_kernel, dim3(1), dim3(256), 0, s, partial, n, sse);
+    return hipGetLastError();
 }
 
 template <class S, int C, int MODE>
 static hipError_t launch_fwd(const FwdDesc &d, hipStream_t s)
 {
-    const int ntiles = (d.count + 31) / 32;
-    int blocks = (ntiles + 3) / 4;
-    if (blocks > 2048)
-        blocks = 2048;
-    if (blocks < 1)
-        blocks = 1;
+    const int blocks = forward_blocks(d.count);
     hipLaunchKernelGGL((forward_kernel<S, C, MODE>), dim3(blocks), dim3(kFwdThreads),
                        FwdLayout<S>::bytes, s, d);
     return hipGetLastError();

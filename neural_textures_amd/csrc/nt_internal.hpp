@@ -150,6 +150,17 @@ struct CodecExpandDesc {
     int64_t start[kMaxExpandLevels + 1]; // prefix of work items (texels x 2)
 };
 
+// Forward-only passes: 256-thread workgroups (four waves) striding over 32-sample tiles,
+// at most kFwdMaxBlocks of them.
+constexpr int kFwdThreads = 256;
+constexpr int kFwdWaves = kFwdThreads / 64;
+constexpr int kFwdMaxBlocks = 2048;
+inline int forward_blocks(int count)
+{
+    const int tiles = (count + 31) / 32, blocks = (tiles + kFwdWaves - 1) / kFwdWaves;
+    return blocks < 1 ? 1 : (blocks > kFwdMaxBlocks ? kFwdMaxBlocks : blocks);
+}
+
 // Forward-only passes: nt_mlp_forward, nt_forward, nt_inference, nt_decode.
 struct FwdDesc {
     MlpDesc mlp;
@@ -168,6 +179,7 @@ struct FwdDesc {
     uint16_t *out16;        // fp16 outputs
     float *out32;           // kFwdInference
     float *sse;             // kFwdInference
+    float *sse_partial;     // kFwdInference: per-wave sums [blocks * kFwdWaves] (NULL: atomics)
     int out_stride;         // outputs per sample
     uint32_t seed;
     float jitter, mip_min, mip_max;
@@ -199,6 +211,9 @@ struct LatentAdamDesc {
     int rec;                 // block record floats (4C+16); 0 = unconstrained
 };
 
+// Sets the message nt_last_error returns (cleared for NT_OK) and returns status.
+int report(int status, const char *fmt, ...);
+
 // ---- launchers (defined next to their kernels) -------------------------------------
 enum ShapeId {
     kShapeRef = 0,   // 12(16) -> 32 -> 32 -> 16, C = 3 (the reference network)
@@ -227,6 +242,8 @@ hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream
 int train_grad_total(int shape);
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s);
 hipError_t launch_forward(int shape, int mode, const FwdDesc &d, hipStream_t s);
+// *sse += the sum of partial[0..n) in a fixed order (one workgroup).
+hipError_t launch_sse_reduce(const float *partial, int n, float *sse, hipStream_t s);
 hipError_t launch_net_adam(const NetAdamDesc &d, hipStream_t s);
 hipError_t launch_latent_adam(const LatentAdamDesc &d, hipStream_t s);
 hipError_t launch_codec_encode(const float *values, int w, int h, int C, uint8_t *blocks,

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 namespace nt_host {
@@ -380,6 +381,8 @@ double run_training_loop(Session &s, const LoopOptions &opt)
     for (int iter = 0; iter < opt.max_iters; ++iter) {
         p.texel_offset_x = rx(region_rng);
         p.texel_offset_y = ry(region_rng);
+        if (iter < opt.start_iter)
+            continue;
         p.feature_adam.learning_rate = base_lr * std::pow(opt.feature_gamma, (float)iter);
         s.train(opt.type);
         s.optimize_network();
@@ -395,6 +398,168 @@ double run_training_loop(Session &s, const LoopOptions &opt)
     }
     p.feature_adam.learning_rate = base_lr;
     return elapsed;
+}
+
+// ---- model container -----------------------------------------------------------------
+
+namespace {
+
+struct HostImage {
+    uint8_t *data = nullptr;
+    size_t bytes = 0;
+    explicit HostImage(size_t n) : bytes(n)
+    {
+        data = static_cast<uint8_t *>(std::aligned_alloc(256, (n + 255) / 256 * 256));
+        if (!data)
+            throw Error("out of host memory for the model image");
+    }
+    ~HostImage() { std::free(data); }
+    HostImage(const HostImage &) = delete;
+    HostImage &operator=(const HostImage &) = delete;
+};
+
+template <class T> void download_into(std::vector<T> &h, const DeviceArray<T> &d)
+{
+    h = d.download();
+}
+
+template <class T> void upload_from(DeviceArray<T> &d, const void *src, size_t count)
+{
+    if (count != d.size())
+        throw Error("model image buffer size does not match the session");
+    if (count)
+        check_hip(hipMemcpy(d.get(), src, count * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+
+} // namespace
+
+void save_model(Session &s, const std::string &path, bool codec)
+{
+    s.synchronize();
+    nt_params &p = s.params();
+    nt_model_info info{};
+    info.contents = NT_MODEL_STATE | (codec ? NT_MODEL_CODEC : 0u);
+    info.num_grids = (int)s.grids.size();
+    info.channels = s.grids[0].channels;
+    for (int g = 0; g < info.num_grids; ++g) {
+        info.width[g] = s.grids[g].width;
+        info.height[g] = s.grids[g].height;
+        info.num_mips[g] = s.grids[g].num_mips;
+    }
+    info.num_layers = (int)s.network.sizes.size() - 1;
+    for (size_t i = 0; i < s.network.sizes.size(); ++i)
+        info.sizes[i] = s.network.sizes[i];
+    info.used_outputs = s.network.used_outputs;
+    info.step = p.step;
+    const size_t bytes = nt_model_bytes(&info);
+    if (!bytes)
+        check(NT_ERR_INVALID_ARGUMENT, "nt_model_bytes");
+
+    // Host copies of everything the image holds (kept alive until nt_model_save).
+    nt_model_data data{};
+    std::vector<std::vector<float>> lat(3 * info.num_grids);
+    std::vector<std::vector<uint8_t>> chains(info.num_grids);
+    for (int g = 0; g < info.num_grids; ++g) {
+        const LatentGrid &lg = s.grids[g];
+        download_into(lat[3 * g], lg.values);
+        download_into(lat[3 * g + 1], lg.moment1);
+        download_into(lat[3 * g + 2], lg.moment2);
+        data.latents[g] = lat[3 * g].data();
+        data.latent_moment1[g] = lat[3 * g + 1].data();
+        data.latent_moment2[g] = lat[3 * g + 2].data();
+        if (codec) {
+            int64_t off[NT_MAX_MIPS];
+            const size_t n = nt_codec_mip_chain_layout(lg.width, lg.height, lg.num_mips, lg.channels, off);
+            DeviceArray<uint8_t> blob(n);
+            for (int m = 0; m < lg.num_mips; ++m) {
+                const int w = std::max(lg.width >> m, 1), h = std::max(lg.height >> m, 1);
+                check(nt_codec_encode(lg.values.get() + lg.mip_offset[m] * lg.channels, w, h, lg.channels,
+                                      blob.get() + off[m], s.stream()),
+                      "nt_codec_encode");
+            }
+            s.synchronize();
+            chains[g] = blob.download();
+            data.codec[g] = chains[g].data();
+        }
+    }
+    const Network &net = s.network;
+    std::vector<std::vector<uint16_t>> wb(2 * info.num_layers);
+    std::vector<std::vector<float>> mom(4 * info.num_layers);
+    for (int l = 0; l < info.num_layers; ++l) {
+        download_into(wb[2 * l], net.weights[l]);
+        download_into(wb[2 * l + 1], net.biases[l]);
+        download_into(mom[4 * l], net.weight_m1[l]);
+        download_into(mom[4 * l + 1], net.weight_m2[l]);
+        download_into(mom[4 * l + 2], net.bias_m1[l]);
+        download_into(mom[4 * l + 3], net.bias_m2[l]);
+        data.weights[l] = wb[2 * l].data();
+        data.biases[l] = wb[2 * l + 1].data();
+        data.weight_moment1[l] = mom[4 * l].data();
+        data.weight_moment2[l] = mom[4 * l + 1].data();
+        data.bias_moment1[l] = mom[4 * l + 2].data();
+        data.bias_moment2[l] = mom[4 * l + 3].data();
+    }
+    HostImage img(bytes);
+    check(nt_model_save(&info, &data, img.data, img.bytes), "nt_model_save");
+    FILE *f = std::fopen(path.c_str(), "wb");
+    if (!f)
+        throw Error("cannot open " + path + " for writing");
+    const size_t wrote = std::fwrite(img.data, 1, img.bytes, f);
+    const bool closed = std::fclose(f) == 0;
+    if (wrote != img.bytes || !closed)
+        throw Error("short write to " + path);
+}
+
+void load_model(Session &s, const std::string &path)
+{
+    FILE *f = std::fopen(path.c_str(), "rb");
+    if (!f)
+        throw Error("cannot open " + path);
+    std::fseek(f, 0, SEEK_END);
+    const long n = std::ftell(f);
+    std::fseek(f, 0, SEEK_SET);
+    if (n <= 0) {
+        std::fclose(f);
+        throw Error(path + " is empty");
+    }
+    HostImage img((size_t)n);
+    const size_t got = std::fread(img.data, 1, img.bytes, f);
+    std::fclose(f);
+    if (got != img.bytes)
+        throw Error("short read from " + path);
+    nt_model_info info{};
+    nt_model_data data{};
+    check(nt_model_load(img.data, img.bytes, &info, &data), "nt_model_load");
+    if (!(info.contents & NT_MODEL_STATE))
+        throw Error(path + " holds no training state");
+    bool same = info.num_grids == (int)s.grids.size() && info.channels == s.grids[0].channels &&
+                info.num_layers == (int)s.network.sizes.size() - 1 && info.used_outputs == s.network.used_outputs;
+    for (int g = 0; same && g < info.num_grids; ++g)
+        same = info.width[g] == s.grids[g].width && info.height[g] == s.grids[g].height &&
+               info.num_mips[g] == s.grids[g].num_mips;
+    for (int i = 0; same && i <= info.num_layers; ++i)
+        same = info.sizes[i] == s.network.sizes[i];
+    if (!same)
+        throw Error(path + ": grids or network differ from this session's");
+    for (int g = 0; g < info.num_grids; ++g) {
+        LatentGrid &lg = s.grids[g];
+        upload_from(lg.values, data.latents[g], lg.values.size());
+        upload_from(lg.moment1, data.latent_moment1[g], lg.moment1.size());
+        upload_from(lg.moment2, data.latent_moment2[g], lg.moment2.size());
+        lg.grads.zero();
+    }
+    Network &net = s.network;
+    for (int l = 0; l < info.num_layers; ++l) {
+        upload_from(net.weights[l], data.weights[l], net.weights[l].size());
+        upload_from(net.biases[l], data.biases[l], net.biases[l].size());
+        upload_from(net.weight_m1[l], data.weight_moment1[l], net.weight_m1[l].size());
+        upload_from(net.weight_m2[l], data.weight_moment2[l], net.weight_m2[l].size());
+        upload_from(net.bias_m1[l], data.bias_moment1[l], net.bias_m1[l].size());
+        upload_from(net.bias_m2[l], data.bias_moment2[l], net.bias_m2[l].size());
+        net.weight_grads[l].zero();
+        net.bias_grads[l].zero();
+    }
+    s.params().step = info.step;
 }
 
 } // namespace nt_host

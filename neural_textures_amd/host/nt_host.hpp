@@ -196,7 +196,15 @@ class Session {
     DeviceArray<float> inference_out_, mse_accum_;
 };
 
+// The model container (nt_model_save / nt_model_load) for a session. save_model writes
+// the training state (latents, Adam moments, step) and, with codec, the latents quantized
+// by nt_codec_encode; load_model restores the training state of an image whose grids and
+// network match the session's.
+void save_model(Session &s, const std::string &path, bool codec);
+void load_model(Session &s, const std::string &path);
+
 struct LoopOptions {
+    int start_iter = 0; // resume: iterations before this one are only replayed for the RNG
     int max_iters = 1000;
     int progress_interval = 1000;
     int region = 512;                 // kTrainingRegionSize, main.cpp:1023

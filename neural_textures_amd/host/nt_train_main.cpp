@@ -4,14 +4,18 @@
 //
 //   nt_train [--mode M] [--grids G] [--channels C] [--hidden H,H,...] [--image S]
 //            [--targets T] [--iters N] [--progress K] [--feature-lr F] [--network-lr F]
-//            [--samples N] [--seed S] [--self-test]
+//            [--samples N] [--seed S] [--resume FILE] [--save FILE] [--self-test]
 //
-// --self-test runs the host-only checks (no GPU) and exits.
+// --self-test runs the host-only checks (no GPU) and exits. --resume continues from the
+// training state of a model image (written by --save of a run with the same settings) at
+// its step, up to --iters; --save writes the model image after training (with the codec
+// chains when the channel count allows the codec: 4, 8, 12 or 16).
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <sstream>
+#include <string>
 
 #include "nt_host.hpp"
 
@@ -54,6 +58,39 @@ int self_test()
     for (float v : t)
         if (!(v >= 0.f && v <= 1.f))
             ++bad;
+    // Model container round trip (host code): a state-only image of a 2-layer network.
+    {
+        nt_model_info info{};
+        info.contents = NT_MODEL_STATE;
+        info.num_grids = 1, info.channels = 3;
+        info.width[0] = 6, info.height[0] = 5, info.num_mips[0] = 3;
+        info.num_layers = 2, info.sizes[0] = 3, info.sizes[1] = 16, info.sizes[2] = 4;
+        info.used_outputs = 4, info.step = 9;
+        const int64_t texels = 6 * 5 + 3 * 2 + 1 * 1;
+        std::vector<float> lat(texels * 3 * 3), mom(2 * (16 * 16 + 16 * 16 + 16 + 4));
+        for (size_t i = 0; i < lat.size(); ++i)
+            lat[i] = (float)i * 0.25f;
+        std::vector<uint16_t> w(16 * 16 + 16 * 16 + 16 + 4, 0x3c00u);
+        nt_model_data d{};
+        d.latents[0] = lat.data(), d.latent_moment1[0] = lat.data() + texels * 3,
+        d.latent_moment2[0] = lat.data() + texels * 6;
+        d.weights[0] = w.data(), d.weights[1] = w.data() + 256, d.biases[0] = w.data() + 512,
+        d.biases[1] = w.data() + 528;
+        d.weight_moment1[0] = d.weight_moment2[0] = d.weight_moment1[1] = d.weight_moment2[1] = mom.data();
+        d.bias_moment1[0] = d.bias_moment2[0] = d.bias_moment1[1] = d.bias_moment2[1] = mom.data();
+        const size_t n = nt_model_bytes(&info);
+        std::vector<uint8_t> buf(n + 256);
+        uint8_t *img = buf.data() + ((256 - ((uintptr_t)buf.data() & 255u)) & 255u);
+        nt_model_info back{};
+        nt_model_data bd{};
+        if (!n || nt_model_save(&info, &d, img, n) != NT_OK || nt_model_load(img, n, &back, &bd) != NT_OK ||
+            back.step != 9 || std::memcmp(bd.latents[0], lat.data(), texels * 12) ||
+            std::memcmp(bd.biases[1], w.data() + 528, 8))
+            ++bad;
+        img[n - 1] ^= 1u; // the last section's checksum must catch this
+        if (nt_model_load(img, n, &back, &bd) != NT_ERR_FORMAT)
+            ++bad;
+    }
     std::printf("self-test: %s (%d failures)\n", bad ? "FAILED" : "ok", bad);
     return bad ? 1 : 0;
 }
@@ -76,6 +113,7 @@ int main(int argc, char **argv)
     LoopOptions loop;
     int image = 2048, targets = 3, samples = 512 * 512;
     uint32_t target_seed = 1u;
+    std::string resume, save;
     loop.max_iters = 1000;
     for (int i = 1; i < argc; ++i) {
         const char *a = argv[i];
@@ -112,6 +150,10 @@ int main(int argc, char **argv)
             samples = std::atoi(next());
         else if (!std::strcmp(a, "--seed"))
             target_seed = (uint32_t)std::strtoul(next(), nullptr, 10);
+        else if (!std::strcmp(a, "--resume"))
+            resume = next();
+        else if (!std::strcmp(a, "--save"))
+            save = next();
         else {
             std::fprintf(stderr, "unknown option %s\n", a);
             return 2;
@@ -145,13 +187,24 @@ int main(int argc, char **argv)
         for (int n : s.network.sizes)
             std::printf(" %d", n);
         std::printf(" (used outputs %d)\n", s.network.used_outputs);
+        if (!resume.empty()) {
+            load_model(s, resume);
+            loop.start_iter = std::min(s.params().step, loop.max_iters);
+            std::printf("Resumed from %s at step %d\n", resume.c_str(), s.params().step);
+        }
         std::printf("Initial inference MSE: %.8f\n", s.inference_mse());
-        std::printf("Starting training for %d iterations\n", loop.max_iters);
+        std::printf("Starting training for %d iterations\n", loop.max_iters - loop.start_iter);
         const double secs = run_training_loop(s, loop);
         const double mse = s.inference_mse();
         std::printf("Train throughput: %.1f samples/s\n",
-                    secs > 0 ? (double)samples * loop.max_iters / secs : 0.0);
+                    secs > 0 ? (double)samples * (loop.max_iters - loop.start_iter) / secs : 0.0);
         std::printf("Inference MSE: %.8f\n", mse);
+        if (!save.empty()) {
+            const bool codec = nt_codec_block_bytes(cfg.channels) != 0;
+            save_model(s, save, codec);
+            std::printf("Saved %s (step %d%s)\n", save.c_str(), s.params().step,
+                        codec ? ", codec chains" : "");
+        }
     } catch (const std::exception &e) {
         std::fprintf(stderr, "nt_train: %s\n", e.what());
         return 1;

@@ -43,7 +43,8 @@ def test_exports_every_declared_function(lib):
 def test_struct_layout_matches_c():
     structs = {"nt_adam": abi.nt_adam, "nt_grid": abi.nt_grid, "nt_latents": abi.nt_latents,
                "nt_mlp": abi.nt_mlp, "nt_texture": abi.nt_texture, "nt_params": abi.nt_params,
-               "nt_codec_grid": abi.nt_codec_grid, "nt_decode_params": abi.nt_decode_params}
+               "nt_codec_grid": abi.nt_codec_grid, "nt_decode_params": abi.nt_decode_params,
+               "nt_model_info": abi.nt_model_info, "nt_model_data": abi.nt_model_data}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for name, cls in structs.items():
         lines.append(f'printf("{name} %zu\\n", sizeof({name}));')

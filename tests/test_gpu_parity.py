@@ -254,6 +254,39 @@ def test_inference(lib, O, shape):
         1e-2 * abs(float(st.inference_mse_accum[0]))
 
 
+def test_inference_sse_fixed_order(lib, O):
+    """With a workspace the SSE is summed in a fixed order: the same bits on every run, and
+    within rounding of the atomic path and of the oracle's float64 sum."""
+    import torch
+    say("case: inference c2 256^2 fixed-order SSE")
+    image = 256
+    st = make_state("c2", image=image, region=(16, 16), seed=9)
+    no = st.net.sizes[-1]
+    st.inference_output = np.zeros(image * image * no, np.float32)
+    st.inference_mse_accum = np.zeros(1, np.float32)
+    assert O.ntref_inference(C.byref(st.params())) == 0
+    gs = gpu_workspace(lib, st.to_torch(), abi.NT_UNCONSTRAINED)
+    need = lib.nt_inference_workspace_bytes(C.byref(gs.params()))
+    assert need == (image * image // 32 // 4) * 4 * 4
+    assert gs.workspace.numel() >= need
+
+    def run(s):
+        s.inference_mse_accum.zero_()
+        nt.check(lib.nt_inference(C.byref(s.params()), None))
+        sync()
+        return to_np(s.inference_mse_accum).copy()
+
+    fixed = [run(gs) for _ in range(3)]
+    assert all(np.array_equal(f.view(np.uint32), fixed[0].view(np.uint32)) for f in fixed)
+    want = float(st.inference_mse_accum[0])
+    assert abs(float(fixed[0][0]) - want) <= 1e-2 * want
+    ws = gs.workspace
+    gs.workspace = None
+    atomic = run(gs)
+    gs.workspace = ws
+    assert abs(float(atomic[0]) - float(fixed[0][0])) <= 1e-5 * float(fixed[0][0])
+
+
 # ---- codec ----------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("w,h,c", [(64, 64, 16), (37, 22, 16), (16, 8, 8), (9, 13, 4), (20, 12, 12)])

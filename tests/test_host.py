@@ -56,3 +56,33 @@ def test_host_training_loop_reduces_mse(program, args):
     before, after = _mse(text, "Initial inference MSE"), _mse(text, "Inference MSE")
     print(f"MSE {before:.6f} -> {after:.6f}", flush=True)
     assert after == after and after < 0.5 * before, text
+
+
+@pytest.mark.gpu
+def test_host_checkpoint_resume(program, tmp_path):
+    """--save after 100 iterations, --resume to 200: the resumed run ends where the
+    uninterrupted 200-iteration run does (the latent-gradient scatter sums with float
+    atomics, so the runs agree to rounding: 2% on the MSE)."""
+    base = [program, "--mode", "0", "--image", "512", "--progress", "100", "--samples", "65536",
+            "--grids", "2", "--channels", "16", "--hidden", "64,64", "--targets", "9",
+            "--feature-lr", "1e-2", "--network-lr", "5e-3"]
+
+    def run(extra):
+        cmd = base + extra
+        print("running", " ".join(cmd), flush=True)
+        out = subprocess.run(cmd, capture_output=True, text=True, timeout=110)
+        text = out.stdout + out.stderr
+        assert out.returncode == 0, text
+        return text
+
+    ck = str(tmp_path / "half.ntm")
+    full = run(["--iters", "200"])
+    half = run(["--iters", "100", "--save", ck])
+    assert "codec chains" in half and os.path.getsize(ck) > 0
+    resumed = run(["--iters", "200", "--resume", ck])
+    assert "at step 100" in resumed and "Completed iteration 200 / 200" in resumed
+    half_mse, start_mse = _mse(half, "\nInference MSE"), _mse(resumed, "Initial inference MSE")
+    assert abs(start_mse - half_mse) <= 1e-4 * half_mse, (half_mse, start_mse)
+    a, b = _mse(full, "\nInference MSE"), _mse(resumed, "\nInference MSE")
+    print(f"MSE uninterrupted {a:.6f}, resumed {b:.6f}", flush=True)
+    assert abs(a - b) <= 0.02 * a
