@@ -257,6 +257,20 @@ int nt_forward(const nt_latents *latents, const nt_mlp *mlp, nt_filter filter,
 /* ---- the block codec -------------------------------------------------------------- */
 
 /*
+ * Initialises every grid's BC6 block records (block_params, all mips) from its
+ * unconstrained latents (values), for the switch from NT_UNCONSTRAINED to
+ * NT_BLOCK_FEATURES training. No reference counterpart: the reference zero-fills its block
+ * records (main.cpp:689-694) and its schedule (main.cpp:1052-1060) would start the block
+ * phase from those. Per 4x4 block: values, clamped to the decode's range [0, 65504]
+ * (unsigned half: negative latents become 0), are mapped to the BC6 decode's linear domain
+ * (train.cu:159-181), each of the 32 two-subset partitions is fitted with one line per
+ * subset, and the partition whose record decodes with the least squared error is written
+ * (mode 0, pixel indices in [0, 1]). Channels 3, 4, 8 or 16; grid sizes multiples of 4
+ * (or at most 4). Block gradients and moments are not touched.
+ */
+int nt_bc6_init(const nt_latents *latents, void *stream);
+
+/*
  * BC6H-style block codec for latent grids (no reference counterpart: the reference has no
  * encoder). Each 4x4 texel block stores, per channel, two fp16 endpoints and sixteen 4-bit
  * indices; a texel decodes to the fp16 whose order key is the BC6H 4-bit interpolation of
@@ -317,8 +331,9 @@ int nt_decode(const nt_decode_params *params, void *stream);
  * reference writes only PNG renders, main.cpp:855-904). It always holds the fp16 network;
  * with NT_MODEL_CODEC the codec-quantized latent mip chains (what nt_decode reads), and
  * with NT_MODEL_STATE the training state (fp32 unconstrained latents, their Adam moments,
- * the network's Adam moments and the step) so a training run resumes from it. Host memory
- * only; moving buffers to and from the device is the caller's.
+ * the network's Adam moments and the step) so a training run resumes from it, and with
+ * NT_MODEL_BLOCKS the BC6 block records and their moments (a run in its block phase).
+ * Host memory only; moving buffers to and from the device is the caller's.
  *
  * Image (little-endian): a 64-byte header {"NTMODEL\0", version, header bytes, section
  * count, contents, image bytes, crc32 of the description and the section table}, the
@@ -330,9 +345,10 @@ int nt_decode(const nt_decode_params *params, void *stream);
 #define NT_MODEL_VERSION 1
 #define NT_MODEL_CODEC 1u /* codec mip chains */
 #define NT_MODEL_STATE 2u /* training state */
+#define NT_MODEL_BLOCKS 4u /* BC6 block records and their Adam moments (with NT_MODEL_STATE) */
 
 typedef struct nt_model_info {
-    uint32_t contents; /* NT_MODEL_CODEC | NT_MODEL_STATE (at least one) */
+    uint32_t contents; /* NT_MODEL_CODEC | NT_MODEL_STATE (at least one) | NT_MODEL_BLOCKS */
     int num_grids;     /* 1..NT_MAX_GRIDS */
     int channels;      /* per grid: 1..16; 4, 8, 12 or 16 with NT_MODEL_CODEC */
     int width[NT_MAX_GRIDS];
@@ -352,6 +368,9 @@ typedef struct nt_model_info {
  *   latents[g], latent_moment1[g], latent_moment2[g]   fp32 [texel][channels] over grid
  *                  g's mips back to back (mip m after the texels of mips < m) (STATE)
  *   weight_moment1/2[l], bias_moment1/2[l]   fp32, as weights / biases (STATE)
+ *   block_params[g]  grid g's block records over its mips, (4 channels + 18) x 4 bytes
+ *                    each (nt_grid's block layout); block_moment1/2[g] the
+ *                    (4 channels + 16)-float moment records (BLOCKS)
  * nt_model_load points these into the image (zero copy) and sets absent ones to NULL.
  */
 typedef struct nt_model_data {
@@ -365,6 +384,9 @@ typedef struct nt_model_data {
     const float *weight_moment2[NT_MAX_LAYERS];
     const float *bias_moment1[NT_MAX_LAYERS];
     const float *bias_moment2[NT_MAX_LAYERS];
+    const float *block_params[NT_MAX_GRIDS];
+    const float *block_moment1[NT_MAX_GRIDS];
+    const float *block_moment2[NT_MAX_GRIDS];
 } nt_model_data;
 
 /* Bytes of the image of a model (0 on a bad description, reason in nt_last_error). */

@@ -28,6 +28,7 @@ NT_ERR_FORMAT = 7
 NT_MODEL_VERSION = 1
 NT_MODEL_CODEC = 1
 NT_MODEL_STATE = 2
+NT_MODEL_BLOCKS = 4
 
 # nt_kernel_type (TrainingKernelType, train.h:22-27)
 NT_UNCONSTRAINED = 0
@@ -142,6 +143,9 @@ class nt_model_data(C.Structure):
         ("weight_moment2", C.c_void_p * NT_MAX_LAYERS),
         ("bias_moment1", C.c_void_p * NT_MAX_LAYERS),
         ("bias_moment2", C.c_void_p * NT_MAX_LAYERS),
+        ("block_params", C.c_void_p * NT_MAX_GRIDS),
+        ("block_moment1", C.c_void_p * NT_MAX_GRIDS),
+        ("block_moment2", C.c_void_p * NT_MAX_GRIDS),
     ]
 
 
@@ -163,6 +167,7 @@ SIGNATURES = {
     "nt_mlp_forward": (C.c_int, [P(nt_mlp), C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
     "nt_forward": (C.c_int, [P(nt_latents), P(nt_mlp), C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                              C.c_void_p, C.c_void_p]),
+    "nt_bc6_init": (C.c_int, [P(nt_latents), C.c_void_p]),
     "nt_codec_block_bytes": (C.c_size_t, [C.c_int]),
     "nt_codec_mip_chain_layout": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, P(C.c_int64)]),
     "nt_codec_encode": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),

@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libnt_hip.so")
 SOURCES = ["nt_api.cpp", "nt_train.hip", "nt_train16.hip", "nt_forward.hip", "nt_adam.hip", "nt_codec.hip",
-           "nt_model.cpp"]
+           "nt_bc6.hip", "nt_model.cpp"]
 HOST_DIR = os.path.join(HERE, "host")
 HOST_SOURCES = ["nt_host.cpp", "nt_train_main.cpp"]
 HOST_PROGRAM = os.path.join(HOST_DIR, "nt_train")

@@ -942,6 +942,49 @@ int nt_forward(const nt_latents *latents, const nt_mlp *mlp, nt_filter filter, c
     return hip_status(launch_forward(shape, mode, d, (hipStream_t)stream), "forward launch");
 }
 
+int nt_bc6_init(const nt_latents *lat, void *stream)
+{
+    if (!lat)
+        return fail(NT_ERR_NULL_POINTER, "latents is NULL");
+    const int C = lat->channels;
+    if (C != 3 && C != 4 && C != 8 && C != 16)
+        return fail(NT_ERR_UNSUPPORTED, "channels %d (3, 4, 8 or 16)", C);
+    if (lat->num_grids < 1 || lat->num_grids > NT_MAX_GRIDS)
+        return fail(NT_ERR_INVALID_ARGUMENT, "num_grids %d outside [1, %d]", lat->num_grids, NT_MAX_GRIDS);
+    Bc6InitDesc d{};
+    d.C = C;
+    int64_t start = 0;
+    for (int gi = 0; gi < lat->num_grids; ++gi) {
+        const nt_grid &g = lat->grids[gi];
+        if (g.width < 1 || g.height < 1 || g.num_mips < 1 || g.num_mips > NT_MAX_MIPS)
+            return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: bad size %dx%d or mip count %d", gi, g.width, g.height,
+                        g.num_mips);
+        if ((g.width & 3 && g.width > 4) || (g.height & 3 && g.height > 4))
+            return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: block storage needs sizes multiple of 4", gi);
+        if (!g.values || !g.block_params)
+            return fail(NT_ERR_NULL_POINTER, "grid %d: values/block_params are NULL", gi);
+        if (((uintptr_t)g.values & 3u) || ((uintptr_t)g.block_params & 3u))
+            return fail(NT_ERR_MISALIGNED, "grid %d: values/block_params must be 4-byte aligned", gi);
+        for (int m = 0; m < g.num_mips; ++m) {
+            if (g.mip_offset[m] < 0 || g.block_offset[m] < 0)
+                return fail(NT_ERR_INVALID_ARGUMENT, "grid %d: negative offset at mip %d", gi, m);
+            const int w = mip_dim_h(g.width, m), h = mip_dim_h(g.height, m);
+            const int nbu = std::max(w >> 2, 1), nbv = std::max(h >> 2, 1);
+            const int k = d.levels++;
+            d.values[k] = g.values + g.mip_offset[m] * C;
+            d.blocks[k] = g.block_params + g.block_offset[m] * (4 * C + 18);
+            d.w[k] = w;
+            d.h[k] = h;
+            d.nbu[k] = nbu;
+            d.start[k] = start;
+            start += (int64_t)nbu * nbv;
+        }
+    }
+    d.start[d.levels] = start;
+    ProfileScope prof((hipStream_t)stream);
+    return hip_status(launch_bc6_init(d, (hipStream_t)stream), "BC6 init launch");
+}
+
 size_t nt_codec_block_bytes(int channels)
 {
     if (channels < 4 || channels > 16 || channels % 4)

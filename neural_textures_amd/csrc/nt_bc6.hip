@@ -1,0 +1,236 @@
+// nt_bc6.hip — BC6 block initialisation from unconstrained latents (nt_bc6_init).
+//
+// The reference zero-fills its BC6 block records (main.cpp:689-694); its schedule's
+// BLOCK_FEATURES phase (main.cpp:1052-1060) would start from those. This kernel instead
+// fits every 4x4 block of every mip to the unconstrained latents trained so far, through
+// the reference's own BC6 decode (train.cu:159-181): values, clamped to the decode's
+// range [0, 65504], are mapped to its linear "y" domain, each of the 32 two-subset
+// partitions (train.cu:20-29) is tried with a
+// line fit per subset, and the partition whose record decodes with the least squared
+// error is written (mode 0: 10-bit endpoints; pixel indices in [0, 1]).
+//
+// One wave per block: lane p + 32 s fits subset s of partition p, the two halves add
+// their errors with one shuffle and an argmin over the 32 partitions (ties to the lowest)
+// picks the record; the two winning lanes write it. Every operation and its order match
+// the oracle's restatement, so records are bit-identical to it.
+#include "nt_internal.hpp"
+
+namespace ntk {
+
+// y whose BC6 decode is v (2^-10 relative at most): the decode is w = (y/1024 - hy)
+// 2^(hy-14) with M = y/1024 - hy in [1 + 2^-10, 2 + 2^-10) for hy >= 1, and w = y 2^-24
+// for y < 2049 (hy = 0).
+__device__ __forceinline__ float bc6_value_to_y(float v)
+{
+    if (v < 2049.f * 0x1p-24f)
+        return ldexpf(v, 24);
+    int e;
+    const float f = frexpf(v, &e);
+    const float m = ldexpf(f, 1);
+    if (m >= 1.f + 0x1p-10f)
+        return 1024.f * (float)(e + 13) + ldexpf(f, 11);
+    if (m < 1.f + 0x1p-11f)
+        return 1024.f * (float)(e + 12) + ldexpf(f, 12);
+    return 1024.f * (float)(e + 13) + 1025.f;
+}
+
+// Line fit of the pixels in `pixels` (a 16-bit mask) of a block v / y [16][C] in LDS:
+// regression of every channel on the widest one, least-squares pixel parameters, the
+// segment's ends as endpoints. Returns the decoded squared error.
+template <int C>
+__device__ __forceinline__ float bc6_fit_subset(const float *v, const float *y, int pixels, int bits,
+                                                float (&e0)[C], float (&e1)[C], float (&x)[16])
+{
+    float sum[C], lo[C], hi[C], mean[C], cov[C], d[C], t[16];
+    int n = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        sum[c] = 0.f;
+        lo[c] = INFINITY;
+        hi[c] = -INFINITY;
+        cov[c] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if ((pixels >> i) & 1) {
+            ++n;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                const float yy = y[i * C + c];
+                sum[c] += yy;
+                lo[c] = fminf(lo[c], yy);
+                hi[c] = fmaxf(hi[c], yy);
+            }
+        }
+    }
+    if (n == 0) {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            e0[c] = e1[c] = 0.f;
+        return 0.f;
+    }
+    int k = 0;
+    float rk = hi[0] - lo[0], mk = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        mean[c] = sum[c] / (float)n;
+        const float r = hi[c] - lo[c];
+        if (c > 0 && r > rk) {
+            k = c;
+            rk = r;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+        mk = c == k ? mean[c] : mk;
+    float var = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if ((pixels >> i) & 1) {
+            const float dk = y[i * C + k] - mk;
+            var = fmaf(dk, dk, var);
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+                cov[c] = fmaf(y[i * C + c] - mean[c], dk, cov[c]);
+        }
+    }
+    float dd = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        d[c] = var > 0.f ? cov[c] / var : 0.f;
+        dd = fmaf(d[c], d[c], dd);
+    }
+    float tlo = INFINITY, thi = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        t[i] = 0.f;
+        if ((pixels >> i) & 1) {
+            float s = 0.f;
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+                s = fmaf(d[c], y[i * C + c] - mean[c], s);
+            t[i] = dd > 0.f ? s / dd : 0.f;
+            tlo = fminf(tlo, t[i]);
+            thi = fmaxf(thi, t[i]);
+        }
+    }
+    // y = q0 + 8 (q1 - q0) x, x in [0, 1] (train.cu:172); q = (31744 e + 32768) 2^-bits.
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const float plo = fmaf(d[c], tlo, mean[c]), phi = fmaf(d[c], thi, mean[c]);
+        const float q1 = plo + ldexpf(phi - plo, -3);
+        e0[c] = (ldexpf(plo, bits) - 32768.f) / 31744.f;
+        e1[c] = (ldexpf(q1, bits) - 32768.f) / 31744.f;
+    }
+    const float span = thi - tlo;
+    float sse = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        x[i] = 0.f;
+        if ((pixels >> i) & 1) {
+            x[i] = span > 0.f ? (t[i] - tlo) / span : 0.f;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                const float r = bc6_decompress(e0[c], e1[c], bits, x[i]) - v[i * C + c];
+                sse = fmaf(r, r, sse);
+            }
+        }
+    }
+    return sse;
+}
+
+template <int C>
+__global__ __launch_bounds__(256) void bc6_init_kernel(Bc6InitDesc d)
+{
+    __shared__ float sv[4][16 * C], sy[4][16 * C];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + wave;
+    const bool active = b < d.start[d.levels];
+    int lev = 0;
+    while (active && lev + 1 < d.levels && b >= d.start[lev + 1])
+        ++lev;
+    const int64_t local = active ? b - d.start[lev] : 0;
+    const int nbu = d.nbu[lev], w = d.w[lev], h = d.h[lev];
+    const int bx = (int)(local % nbu), by = (int)(local / nbu);
+    int valid = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        valid |= (4 * bx + (i & 3) < w && 4 * by + (i >> 2) < h) ? 1 << i : 0;
+    if (active) {
+        const float *vals = d.values[lev];
+        for (int idx = lane; idx < 16 * C; idx += 64) {
+            const int i = idx / C, c = idx % C;
+            const int tx = 4 * bx + (i & 3), ty = 4 * by + (i >> 2);
+            const bool ok = (valid >> i) & 1;
+            // Target range of the decode: [0, 65504] (unsigned half).
+            const float v = ok ? fminf(fmaxf(vals[((int64_t)ty * w + tx) * C + c], 0.f), 65504.f) : 0.f;
+            sv[wave][idx] = v;
+            sy[wave][idx] = ok ? bc6_value_to_y(v) : 0.f;
+        }
+    }
+    __syncthreads();
+    if (!active)
+        return;
+    constexpr int kBits = 10; // mode 0
+    const int p = lane & 31, s = lane >> 5, mask = bc6_partition_mask(p);
+    const int pixels = valid & (s ? mask : ~mask) & 0xFFFF;
+    float e0[C], e1[C], x[16];
+    const float sse = bc6_fit_subset<C>(sv[wave], sy[wave], pixels, kBits, e0, e1, x);
+    float tot = sse + __shfl_xor(sse, 32);
+    if (tot != tot)
+        tot = INFINITY;
+    float bt = tot;
+    int bp = p;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        const float ot = __shfl_xor(bt, off);
+        const int op = __shfl_xor(bp, off);
+        if (ot < bt || (ot == bt && op < bp)) {
+            bt = ot;
+            bp = op;
+        }
+    }
+    if (p != bp)
+        return;
+    float *rec = d.blocks[lev] + local * (4 * C + 18);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        rec[2 * s * C + c] = e0[c];
+        rec[(2 * s + 1) * C + c] = e1[c];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (((mask >> i) & 1) == s)
+            rec[4 * C + i] = ((valid >> i) & 1) ? x[i] : 0.f;
+    if (s == 0) {
+        rec[4 * C + 16] = __int_as_float(p);
+        rec[4 * C + 17] = __int_as_float(0);
+    }
+}
+
+hipError_t launch_bc6_init(const Bc6InitDesc &d, hipStream_t s)
+{
+    const int64_t blocks = d.start[d.levels];
+    if (blocks <= 0)
+        return hipSuccess;
+    const dim3 grid((unsigned)((blocks + 3) / 4));
+    switch (d.C) {
+    case 3:
+        hipLaunchKernelGGL(bc6_init_kernel<3>, grid, dim3(256), 0, s, d);
+        break;
+    case 4:
+        hipLaunchKernelGGL(bc6_init_kernel<4>, grid, dim3(256), 0, s, d);
+        break;
+    case 8:
+        hipLaunchKernelGGL(bc6_init_kernel<8>, grid, dim3(256), 0, s, d);
+        break;
+    case 16:
+        hipLaunchKernelGGL(bc6_init_kernel<16>, grid, dim3(256), 0, s, d);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+} // namespace ntk

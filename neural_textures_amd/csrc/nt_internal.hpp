@@ -150,6 +150,16 @@ struct CodecExpandDesc {
     int64_t start[kMaxExpandLevels + 1]; // prefix of work items (texels x 2)
 };
 
+// BC6 block initialisation (nt_bc6_init): every (grid, mip) level, blocks numbered over
+// all levels (start = prefix of block counts).
+struct Bc6InitDesc {
+    int C, levels;
+    const float *values[kMaxExpandLevels]; // the level's first texel
+    float *blocks[kMaxExpandLevels];       // the level's first block record
+    int w[kMaxExpandLevels], h[kMaxExpandLevels], nbu[kMaxExpandLevels];
+    int64_t start[kMaxExpandLevels + 1];
+};
+
 // Forward-only passes: 256-thread workgroups (four waves) striding over 32-sample tiles,
 // at most kFwdMaxBlocks of them.
 constexpr int kFwdThreads = 256;
@@ -251,5 +261,6 @@ hipError_t launch_codec_encode(const float *values, int w, int h, int C, uint8_t
 hipError_t launch_codec_decode(const uint8_t *blocks, int w, int h, int C, float *values,
                                hipStream_t s);
 hipError_t launch_codec_expand(const CodecExpandDesc &d, hipStream_t s);
+hipError_t launch_bc6_init(const Bc6InitDesc &d, hipStream_t s);
 
 } // namespace ntk

@@ -23,7 +23,7 @@ namespace {
 constexpr char kMagic[8] = {'N', 'T', 'M', 'O', 'D', 'E', 'L', '\0'};
 constexpr int kDescInts = 32;
 constexpr uint64_t kSectionAlign = 256;
-constexpr int kMaxSections = NT_MAX_GRIDS * 4 + NT_MAX_LAYERS * 6;
+constexpr int kMaxSections = NT_MAX_GRIDS * 7 + NT_MAX_LAYERS * 6;
 constexpr int kMaxSize = 1024;     // network widths
 constexpr int kMaxExtent = 1 << 16; // grid widths / heights
 
@@ -38,14 +38,18 @@ enum Section : uint32_t {
     kWeightM2 = 8,
     kBiasM1 = 9,
     kBiasM2 = 10,
+    kBlocks = 11,
+    kBlockM1 = 12,
+    kBlockM2 = 13,
 };
 
 const char *section_name(uint32_t t)
 {
-    static const char *names[] = {"?",        "codec",          "weights",        "biases",
-                                  "latents",  "latent_moment1", "latent_moment2", "weight_moment1",
-                                  "weight_moment2", "bias_moment1", "bias_moment2"};
-    return t <= kBiasM2 ? names[t] : "?";
+    static const char *names[] = {"?",              "codec",         "weights",        "biases",
+                                  "latents",        "latent_moment1", "latent_moment2", "weight_moment1",
+                                  "weight_moment2", "bias_moment1",  "bias_moment2",   "block_params",
+                                  "block_moment1",  "block_moment2"};
+    return t <= kBlockM2 ? names[t] : "?";
 }
 
 struct Header {
@@ -118,6 +122,16 @@ uint32_t crc32c(const void *data, size_t n, uint32_t crc = 0)
 uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 uint64_t pad16(int x) { return (uint64_t)((x + 15) / 16 * 16); }
 
+uint64_t chain_blocks(int w, int h, int mips)
+{
+    uint64_t n = 0;
+    for (int m = 0; m < mips; ++m) {
+        const int wm = (w >> m) > 0 ? (w >> m) : 1, hm = (h >> m) > 0 ? (h >> m) : 1;
+        n += (uint64_t)((wm >> 2) > 0 ? (wm >> 2) : 1) * (uint64_t)((hm >> 2) > 0 ? (hm >> 2) : 1);
+    }
+    return n;
+}
+
 uint64_t chain_texels(int w, int h, int mips)
 {
     uint64_t n = 0;
@@ -171,9 +185,11 @@ void unpack_info(const int32_t (&d)[kDescInts], nt_model_info *m)
 
 int check_info(const nt_model_info &m, int status)
 {
-    const uint32_t all = NT_MODEL_CODEC | NT_MODEL_STATE;
-    if (!m.contents || (m.contents & ~all))
+    const uint32_t all = NT_MODEL_CODEC | NT_MODEL_STATE | NT_MODEL_BLOCKS;
+    if (!(m.contents & (NT_MODEL_CODEC | NT_MODEL_STATE)) || (m.contents & ~all))
         return ntk::report(status, "contents 0x%x (need NT_MODEL_CODEC and/or NT_MODEL_STATE)", m.contents);
+    if ((m.contents & NT_MODEL_BLOCKS) && !(m.contents & NT_MODEL_STATE))
+        return ntk::report(status, "NT_MODEL_BLOCKS needs NT_MODEL_STATE");
     if (m.num_grids < 1 || m.num_grids > NT_MAX_GRIDS)
         return ntk::report(status, "num_grids %d (1..%d)", m.num_grids, NT_MAX_GRIDS);
     if (m.channels < 1 || m.channels > 16)
@@ -185,6 +201,8 @@ int check_info(const nt_model_info &m, int status)
             return ntk::report(status, "grid %d size %dx%d (1..%d)", g, m.width[g], m.height[g], kMaxExtent);
         if (m.num_mips[g] < 1 || m.num_mips[g] > NT_MAX_MIPS)
             return ntk::report(status, "grid %d num_mips %d (1..%d)", g, m.num_mips[g], NT_MAX_MIPS);
+        if ((m.contents & NT_MODEL_BLOCKS) && (((m.width[g] & 3) && m.width[g] > 4) || ((m.height[g] & 3) && m.height[g] > 4)))
+            return ntk::report(status, "grid %d: block records need sizes multiple of 4", g);
     }
     if (m.num_layers < 1 || m.num_layers > NT_MAX_LAYERS)
         return ntk::report(status, "num_layers %d (1..%d)", m.num_layers, NT_MAX_LAYERS);
@@ -239,6 +257,13 @@ void plan_sections(const nt_model_info &m, Plan *p)
             add(kBiasM2, l, bb);
         }
     }
+    if (m.contents & NT_MODEL_BLOCKS)
+        for (int g = 0; g < m.num_grids; ++g) {
+            const uint64_t nb = chain_blocks(m.width[g], m.height[g], m.num_mips[g]);
+            add(kBlocks, g, nb * (4 * m.channels + 18) * 4);
+            add(kBlockM1, g, nb * (4 * m.channels + 16) * 4);
+            add(kBlockM2, g, nb * (4 * m.channels + 16) * 4);
+        }
     uint64_t off = align_up(kTableOff + (uint64_t)p->n * sizeof(Entry), kSectionAlign);
     for (int i = 0; i < p->n; ++i) {
         p->e[i].offset = off;
@@ -269,8 +294,14 @@ const void **slot(nt_model_data *d, uint32_t type, uint32_t i)
         return (const void **)&d->weight_moment2[i];
     case kBiasM1:
         return (const void **)&d->bias_moment1[i];
-    default:
+    case kBiasM2:
         return (const void **)&d->bias_moment2[i];
+    case kBlocks:
+        return (const void **)&d->block_params[i];
+    case kBlockM1:
+        return (const void **)&d->block_moment1[i];
+    default:
+        return (const void **)&d->block_moment2[i];
     }
 }
 

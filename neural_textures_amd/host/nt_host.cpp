@@ -368,6 +368,18 @@ double Session::inference_mse()
     return (double)sse / (pixels * std::max(1, packed_channel_count(textures)));
 }
 
+void Session::init_blocks()
+{
+    if (!has_blocks())
+        throw Error("the session has no block storage");
+    check(nt_bc6_init(&params_.latents, stream_), "nt_bc6_init");
+    for (LatentGrid &g : grids) {
+        g.block_grads.zero();
+        g.block_moment1.zero();
+        g.block_moment2.zero();
+    }
+}
+
 double run_training_loop(Session &s, const LoopOptions &opt)
 {
     nt_params &p = s.params();
@@ -383,11 +395,25 @@ double run_training_loop(Session &s, const LoopOptions &opt)
         p.texel_offset_y = ry(region_rng);
         if (iter < opt.start_iter)
             continue;
-        p.feature_adam.learning_rate = base_lr * std::pow(opt.feature_gamma, (float)iter);
-        s.train(opt.type);
+        nt_kernel_type type = opt.type;
+        if (opt.unconstrained_iters >= 0) {
+            const int block_end = opt.unconstrained_iters + opt.block_iters;
+            type = iter < opt.unconstrained_iters ? NT_UNCONSTRAINED
+                   : iter < block_end             ? NT_BLOCK_FEATURES
+                                                  : NT_FINALIZE;
+            // Entering the block phase (or a finalize phase with no block phase before it).
+            if (iter == opt.unconstrained_iters && type != NT_UNCONSTRAINED)
+                s.init_blocks();
+        }
+        if (type == NT_BLOCK_FEATURES)
+            p.feature_adam.learning_rate =
+                base_lr * std::pow(opt.block_gamma, (float)(iter - opt.unconstrained_iters));
+        else
+            p.feature_adam.learning_rate = base_lr * std::pow(opt.feature_gamma, (float)iter);
+        s.train(type);
         s.optimize_network();
-        if (opt.type != NT_FINALIZE)
-            s.optimize_features(opt.type);
+        if (type != NT_FINALIZE)
+            s.optimize_features(type);
         p.step++;
         if ((iter + 1) % opt.progress_interval == 0 || iter + 1 == opt.max_iters) {
             s.synchronize();
@@ -438,7 +464,7 @@ void save_model(Session &s, const std::string &path, bool codec)
     s.synchronize();
     nt_params &p = s.params();
     nt_model_info info{};
-    info.contents = NT_MODEL_STATE | (codec ? NT_MODEL_CODEC : 0u);
+    info.contents = NT_MODEL_STATE | (codec ? NT_MODEL_CODEC : 0u) | (s.has_blocks() ? NT_MODEL_BLOCKS : 0u);
     info.num_grids = (int)s.grids.size();
     info.channels = s.grids[0].channels;
     for (int g = 0; g < info.num_grids; ++g) {
@@ -457,7 +483,7 @@ void save_model(Session &s, const std::string &path, bool codec)
 
     // Host copies of everything the image holds (kept alive until nt_model_save).
     nt_model_data data{};
-    std::vector<std::vector<float>> lat(3 * info.num_grids);
+    std::vector<std::vector<float>> lat(6 * info.num_grids);
     std::vector<std::vector<uint8_t>> chains(info.num_grids);
     for (int g = 0; g < info.num_grids; ++g) {
         const LatentGrid &lg = s.grids[g];
@@ -467,6 +493,15 @@ void save_model(Session &s, const std::string &path, bool codec)
         data.latents[g] = lat[3 * g].data();
         data.latent_moment1[g] = lat[3 * g + 1].data();
         data.latent_moment2[g] = lat[3 * g + 2].data();
+        if (info.contents & NT_MODEL_BLOCKS) {
+            std::vector<float> *b = &lat[3 * info.num_grids + 3 * g];
+            download_into(b[0], lg.block_params);
+            download_into(b[1], lg.block_moment1);
+            download_into(b[2], lg.block_moment2);
+            data.block_params[g] = b[0].data();
+            data.block_moment1[g] = b[1].data();
+            data.block_moment2[g] = b[2].data();
+        }
         if (codec) {
             int64_t off[NT_MAX_MIPS];
             const size_t n = nt_codec_mip_chain_layout(lg.width, lg.height, lg.num_mips, lg.channels, off);
@@ -547,6 +582,14 @@ void load_model(Session &s, const std::string &path)
         upload_from(lg.moment1, data.latent_moment1[g], lg.moment1.size());
         upload_from(lg.moment2, data.latent_moment2[g], lg.moment2.size());
         lg.grads.zero();
+        if (info.contents & NT_MODEL_BLOCKS) {
+            if (!s.has_blocks())
+                throw Error(path + " holds BC6 block state; this session has no block storage");
+            upload_from(lg.block_params, data.block_params[g], lg.block_params.size());
+            upload_from(lg.block_moment1, data.block_moment1[g], lg.block_moment1.size());
+            upload_from(lg.block_moment2, data.block_moment2[g], lg.block_moment2.size());
+            lg.block_grads.zero();
+        }
     }
     Network &net = s.network;
     for (int l = 0; l < info.num_layers; ++l) {

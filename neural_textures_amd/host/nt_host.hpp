@@ -179,6 +179,10 @@ class Session {
     void optimize_features(nt_kernel_type type);  // InvokeOptimizeFeatures
     // InvokeInference + the MSE of main.cpp:1090-1109 (SSE / (pixels * packed channels)).
     double inference_mse();
+    // Start of the BC6 block phase: block records fitted to the unconstrained latents
+    // (nt_bc6_init), block gradients and moments cleared. Needs block storage.
+    void init_blocks();
+    bool has_blocks() const { return !grids.empty() && grids[0].block_params.size() > 0; }
 
     nt_params &params() { return params_; }
     hipStream_t stream() const { return stream_; }
@@ -206,6 +210,14 @@ void load_model(Session &s, const std::string &path);
 struct LoopOptions {
     int start_iter = 0; // resume: iterations before this one are only replayed for the RNG
     int max_iters = 1000;
+    // Phase schedule of main.cpp:1018-1064 when unconstrained_iters >= 0: iterations below
+    // it train the unconstrained latents (type NT_UNCONSTRAINED), the next block_iters the
+    // BC6 block latents (NT_BLOCK_FEATURES, learning rate decayed by block_gamma from the
+    // phase start, blocks initialised by Session::init_blocks), the rest the network only
+    // (NT_FINALIZE). Otherwise every iteration uses `type`.
+    int unconstrained_iters = -1;
+    int block_iters = 0;
+    float block_gamma = 0.9999f; // kBlockFeatureGamma, main.cpp:1028
     int progress_interval = 1000;
     int region = 512;                 // kTrainingRegionSize, main.cpp:1023
     float feature_gamma = 0.9995f;    // kUnconstrainedFeatureGamma, main.cpp:1027

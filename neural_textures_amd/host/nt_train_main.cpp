@@ -4,9 +4,14 @@
 //
 //   nt_train [--mode M] [--grids G] [--channels C] [--hidden H,H,...] [--image S]
 //            [--targets T] [--iters N] [--progress K] [--feature-lr F] [--network-lr F]
-//            [--samples N] [--seed S] [--resume FILE] [--save FILE] [--self-test]
+//            [--samples N] [--seed S] [--phases U,B] [--resume FILE] [--save FILE]
+//            [--self-test]
 //
-// --self-test runs the host-only checks (no GPU) and exits. --resume continues from the
+// --self-test runs the host-only checks (no GPU) and exits. --phases U,B runs the
+// reference's three-phase schedule (main.cpp:1018-1064; 5000,10000 there): U unconstrained
+// iterations, B BC6 block iterations starting from nt_bc6_init, then FINALIZE (network
+// only) up to --iters. Without it every iteration trains the unconstrained latents, as the
+// reference loop currently does (main.cpp:1066-1069). --resume continues from the
 // training state of a model image (written by --save of a run with the same settings) at
 // its step, up to --iters; --save writes the model image after training (with the codec
 // chains when the channel count allows the codec: 4, 8, 12 or 16).
@@ -152,6 +157,16 @@ int main(int argc, char **argv)
             target_seed = (uint32_t)std::strtoul(next(), nullptr, 10);
         else if (!std::strcmp(a, "--resume"))
             resume = next();
+        else if (!std::strcmp(a, "--phases")) {
+            const std::vector<int> ph = parse_list(next());
+            if (ph.size() != 2 || ph[0] < 0 || ph[1] < 0) {
+                std::fprintf(stderr, "--phases needs U,B (two counts)\n");
+                return 2;
+            }
+            loop.unconstrained_iters = ph[0];
+            loop.block_iters = ph[1];
+            cfg.with_blocks = true;
+        }
         else if (!std::strcmp(a, "--save"))
             save = next();
         else {

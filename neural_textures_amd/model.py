@@ -14,7 +14,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import abi, check, load
-from .params import Grid, Network, codec_chain_layout, mip_chain_layout
+from .params import Grid, Network, block_chain_layout, codec_chain_layout, mip_chain_layout
 
 
 def aligned_bytes(nbytes: int, align: int = 256) -> np.ndarray:
@@ -40,8 +40,9 @@ class CodecChain:
 
 @dataclass
 class Model:
-    """What a model image holds. `grids` (with values/moment1/moment2) only for training
-    state; `codec` only for images with codec chains."""
+    """What a model image holds. `grids` (with values/moment1/moment2, and block_params /
+    block_moment1/2 when present) only for training state; `codec` only for images with
+    codec chains."""
     net: Network
     channels: int
     shapes: list  # (width, height, num_mips) per grid
@@ -51,7 +52,9 @@ class Model:
 
     @property
     def contents(self) -> int:
-        return (abi.NT_MODEL_CODEC if self.codec else 0) | (abi.NT_MODEL_STATE if self.grids else 0)
+        blocks = bool(self.grids) and self.grids[0].block_params is not None
+        return ((abi.NT_MODEL_CODEC if self.codec else 0) | (abi.NT_MODEL_STATE if self.grids else 0)
+                | (abi.NT_MODEL_BLOCKS if blocks else 0))
 
 
 def _host(a, dtype) -> np.ndarray:
@@ -109,6 +112,10 @@ def model_image(m: Model) -> np.ndarray:
         d.latents[g] = ptr(grid.values, np.float32)
         d.latent_moment1[g] = ptr(grid.moment1, np.float32)
         d.latent_moment2[g] = ptr(grid.moment2, np.float32)
+        if m.contents & abi.NT_MODEL_BLOCKS:
+            d.block_params[g] = ptr(grid.block_params, np.float32)
+            d.block_moment1[g] = ptr(grid.block_moment1, np.float32)
+            d.block_moment2[g] = ptr(grid.block_moment2, np.float32)
     out = aligned_bytes(n)
     check(lib.nt_model_save(C.byref(info), C.byref(d), out.ctypes.data, out.nbytes))
     return out
@@ -176,11 +183,18 @@ def load_model(src) -> Model:
     if state:
         for g, (w, h, mips) in enumerate(shapes):
             n = mip_chain_layout(w, h, mips)[1] * ch
-            m.grids.append(Grid(w, h, mips, ch,
-                                values=arr(d.latents[g], np.float32, n),
-                                grads=np.zeros(n, np.float32),
-                                moment1=arr(d.latent_moment1[g], np.float32, n),
-                                moment2=arr(d.latent_moment2[g], np.float32, n)))
+            grid = Grid(w, h, mips, ch,
+                        values=arr(d.latents[g], np.float32, n),
+                        grads=np.zeros(n, np.float32),
+                        moment1=arr(d.latent_moment1[g], np.float32, n),
+                        moment2=arr(d.latent_moment2[g], np.float32, n))
+            if info.contents & abi.NT_MODEL_BLOCKS:
+                nb = block_chain_layout(w, h, mips)[1]
+                grid.block_params = arr(d.block_params[g], np.float32, nb * (4 * ch + 18))
+                grid.block_grads = np.zeros(nb * (4 * ch + 16), np.float32)
+                grid.block_moment1 = arr(d.block_moment1[g], np.float32, nb * (4 * ch + 16))
+                grid.block_moment2 = arr(d.block_moment2[g], np.float32, nb * (4 * ch + 16))
+            m.grids.append(grid)
     return m
 
 

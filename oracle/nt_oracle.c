@@ -480,6 +480,188 @@ void ntref_scatter_bc6(const nt_latents *lat, const float uvz[3], const uint16_t
     scatter_bc6(lat, uvz, dinput);
 }
 
+/* ---- BC6 block initialisation from unconstrained latents ----------------------------
+ * No reference counterpart: the reference zero-fills its block records
+ * (main.cpp:689-694) and its schedule would switch to BLOCK_FEATURES from those
+ * (main.cpp:1052-1060). This is the initialisation nt_bc6_init performs. */
+
+float ntref_bc6_value_to_y(float v)
+{
+    /* Inverse of the decode y -> w of train.cu:167-181: for hy >= 1 the decode is
+     * w = (y/1024 - hy) 2^(hy-14) with M = y/1024 - hy in [1 + 2^-10, 2 + 2^-10); for
+     * hy = 0 (y < 2049) it is linear, w = y 2^-24. With v = f 2^e (f in [0.5, 1)): M = 2f
+     * at hy = e + 13, or M = 4f at hy = e + 12 when 2f < 1 + 2^-11. Values in between
+     * (2f in [1 + 2^-11, 1 + 2^-10)) have no exact y and map to the start of the upper
+     * range (2^-10 relative error at most). */
+    if (v < 2049.f * 0x1p-24f)
+        return ldexpf(v, 24);
+    int e;
+    const float f = frexpf(v, &e);
+    const float m = ldexpf(f, 1);
+    if (m >= 1.f + 0x1p-10f)
+        return 1024.f * (float)(e + 13) + ldexpf(f, 11);
+    if (m < 1.f + 0x1p-11f)
+        return 1024.f * (float)(e + 12) + ldexpf(f, 12);
+    return 1024.f * (float)(e + 13) + 1025.f;
+}
+
+float ntref_bc6_fit_subset(const float *v, const float *y, int C, int pixels, int bits, float *e0,
+                           float *e1, float *x)
+{
+    float sum[16], lo[16], hi[16], mean[16], cov[16], d[16], t[16];
+    int n = 0;
+    for (int c = 0; c < C; ++c) {
+        sum[c] = 0.f;
+        lo[c] = INFINITY;
+        hi[c] = -INFINITY;
+        cov[c] = 0.f;
+    }
+    for (int i = 0; i < 16; ++i) {
+        if (!((pixels >> i) & 1))
+            continue;
+        ++n;
+        for (int c = 0; c < C; ++c) {
+            const float yy = y[i * C + c];
+            sum[c] += yy;
+            lo[c] = fminf(lo[c], yy);
+            hi[c] = fmaxf(hi[c], yy);
+        }
+    }
+    if (n == 0) {
+        for (int c = 0; c < C; ++c)
+            e0[c] = e1[c] = 0.f;
+        return 0.f;
+    }
+    int k = 0;
+    for (int c = 0; c < C; ++c) {
+        mean[c] = sum[c] / (float)n;
+        if (c > 0 && hi[c] - lo[c] > hi[k] - lo[k])
+            k = c;
+    }
+    /* Regression of every channel on channel k (the widest), then the least-squares
+     * parameter of each pixel along that direction. */
+    float var = 0.f;
+    for (int i = 0; i < 16; ++i) {
+        if (!((pixels >> i) & 1))
+            continue;
+        const float dk = y[i * C + k] - mean[k];
+        var = fmaf(dk, dk, var);
+        for (int c = 0; c < C; ++c)
+            cov[c] = fmaf(y[i * C + c] - mean[c], dk, cov[c]);
+    }
+    float dd = 0.f;
+    for (int c = 0; c < C; ++c) {
+        d[c] = var > 0.f ? cov[c] / var : 0.f;
+        dd = fmaf(d[c], d[c], dd);
+    }
+    float tlo = INFINITY, thi = -INFINITY;
+    for (int i = 0; i < 16; ++i) {
+        if (!((pixels >> i) & 1))
+            continue;
+        float s = 0.f;
+        for (int c = 0; c < C; ++c)
+            s = fmaf(d[c], y[i * C + c] - mean[c], s);
+        t[i] = dd > 0.f ? s / dd : 0.f;
+        tlo = fminf(tlo, t[i]);
+        thi = fmaxf(thi, t[i]);
+    }
+    /* Segment ends -> endpoints: y = q0 + 8 (q1 - q0) x with x in [0, 1] (train.cu:172),
+     * q = (31744 e + 32768) 2^-bits (train.cu:161-166). */
+    for (int c = 0; c < C; ++c) {
+        const float plo = fmaf(d[c], tlo, mean[c]), phi = fmaf(d[c], thi, mean[c]);
+        const float q1 = plo + ldexpf(phi - plo, -3);
+        e0[c] = (ldexpf(plo, bits) - 32768.f) / 31744.f;
+        e1[c] = (ldexpf(q1, bits) - 32768.f) / 31744.f;
+    }
+    const float span = thi - tlo;
+    float sse = 0.f;
+    for (int i = 0; i < 16; ++i) {
+        if (!((pixels >> i) & 1))
+            continue;
+        x[i] = span > 0.f ? (t[i] - tlo) / span : 0.f;
+        for (int c = 0; c < C; ++c) {
+            const float r = ntref_bc6_decompress(e0[c], e1[c], bits, x[i]) - v[i * C + c];
+            sse = fmaf(r, r, sse);
+        }
+    }
+    return sse;
+}
+
+void ntref_bc6_init_block(const float *v, int C, int valid, float *rec)
+{
+    float y[16 * 16], e[2][2][16], x[2][16];
+    const int bits = ntref_bc6_partition_bits[0];
+    /* The decode reaches [0, 65504] (the unsigned half range; negative values only as
+     * y < 0 in its tiny linear range): the fit targets the values clamped to it. */
+    float vc[16 * 16];
+    for (int i = 0; i < 16 * C; ++i) {
+        vc[i] = fminf(fmaxf(v[i], 0.f), 65504.f);
+        y[i] = ((valid >> (i / C)) & 1) ? ntref_bc6_value_to_y(vc[i]) : 0.f;
+    }
+    v = vc;
+    int best = 0;
+    float best_sse = INFINITY;
+    for (int p = 0; p < 32; ++p) {
+        const int mask = ntref_bc6_partition_sets[p];
+        const float s0 = ntref_bc6_fit_subset(v, y, C, valid & ~mask & 0xFFFF, bits, e[0][0], e[0][1], x[0]);
+        const float s1 = ntref_bc6_fit_subset(v, y, C, valid & mask, bits, e[1][0], e[1][1], x[1]);
+        float tot = s0 + s1;
+        if (tot != tot)
+            tot = INFINITY;
+        if (p == 0 || tot < best_sse) {
+            best = p;
+            best_sse = tot;
+        }
+    }
+    const int mask = ntref_bc6_partition_sets[best];
+    for (int s = 0; s < 2; ++s) {
+        const int pixels = valid & (s ? mask : ~mask) & 0xFFFF;
+        ntref_bc6_fit_subset(v, y, C, pixels, bits, e[s][0], e[s][1], x[s]);
+        for (int c = 0; c < C; ++c) {
+            rec[2 * s * C + c] = e[s][0][c];
+            rec[(2 * s + 1) * C + c] = e[s][1][c];
+        }
+    }
+    for (int i = 0; i < 16; ++i) {
+        const int s = (mask >> i) & 1;
+        rec[4 * C + i] = ((valid >> i) & 1) ? x[s][i] : 0.f;
+    }
+    const int32_t part = best, mode = 0;
+    memcpy(rec + 4 * C + 16, &part, 4);
+    memcpy(rec + 4 * C + 17, &mode, 4);
+}
+
+int ntref_bc6_init(const nt_latents *lat)
+{
+    const int C = lat->channels;
+    if (C < 1 || C > 16)
+        return 1;
+    for (int g = 0; g < lat->num_grids; ++g) {
+        const nt_grid *gr = &lat->grids[g];
+        if (!gr->values || !gr->block_params)
+            return 2;
+        for (int m = 0; m < gr->num_mips; ++m) {
+            const int w = mip_dim(gr->width, m), h = mip_dim(gr->height, m);
+            const int nbu = (w >> 2) > 0 ? (w >> 2) : 1, nbv = (h >> 2) > 0 ? (h >> 2) : 1;
+            for (int by = 0; by < nbv; ++by)
+                for (int bx = 0; bx < nbu; ++bx) {
+                    float v[16 * 16];
+                    int valid = 0;
+                    for (int i = 0; i < 16; ++i) {
+                        const int tx = 4 * bx + (i & 3), ty = 4 * by + (i >> 2);
+                        const int ok = tx < w && ty < h;
+                        valid |= ok << i;
+                        for (int c = 0; c < C; ++c)
+                            v[i * C + c] = ok ? gr->values[(gr->mip_offset[m] + (int64_t)ty * w + tx) * C + c] : 0.f;
+                    }
+                    float *rec = gr->block_params + (gr->block_offset[m] + (int64_t)by * nbu + bx) * (4 * C + 18);
+                    ntref_bc6_init_block(v, C, valid, rec);
+                }
+        }
+    }
+    return 0;
+}
+
 /* ---- MLP (mlp.h:18-362) ------------------------------------------------------------ */
 
 void ntref_mlp_forward_one(const nt_mlp *mlp, const uint16_t *in, uint16_t *acts,

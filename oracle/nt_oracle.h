@@ -73,6 +73,18 @@ float ntref_bc6_decompress(float e0, float e1, int bits, float x);
 extern const int ntref_bc6_partition_sets[32];
 extern const int ntref_bc6_partition_bits[10];
 
+/* BC6 block initialisation from unconstrained latents (nt_bc6_init; no reference
+ * counterpart). ntref_bc6_value_to_y inverts the BC6 decode's y -> value map;
+ * ntref_bc6_fit_subset fits one partition subset (pixel mask) of a block [16][C] with a
+ * line in y space and returns its decoded squared error; ntref_bc6_init_block picks the
+ * partition of least total error and writes a block record; ntref_bc6_init does every
+ * block of every mip of every grid (block_params from values). */
+float ntref_bc6_value_to_y(float v);
+float ntref_bc6_fit_subset(const float *v, const float *y, int C, int pixels, int bits, float *e0,
+                           float *e1, float *x);
+void ntref_bc6_init_block(const float *v, int C, int valid, float *rec);
+int ntref_bc6_init(const nt_latents *lat);
+
 /*
  * MLP forward for one sample (mlp.h:18-99). in: sizes[0] fp16. acts (optional): the
  * fp16 input of every layer, layer l at acts + l*64 (64 = max padded width), zero-padded.

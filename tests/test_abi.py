@@ -124,6 +124,14 @@ def test_argument_errors_enqueue_nothing(lib):
     buf = np.zeros(64, np.float32)
     assert lib.nt_codec_encode(buf.ctypes.data, 4, 4, 3, buf.ctypes.data, None) == abi.NT_ERR_INVALID_ARGUMENT
     assert lib.nt_mlp_forward(None, None, None, 1, None) == abi.NT_ERR_NULL_POINTER
+    assert lib.nt_bc6_init(None, None) == abi.NT_ERR_NULL_POINTER
+    lat = st.params().latents  # no block_params
+    assert lib.nt_bc6_init(C.byref(lat), None) == abi.NT_ERR_NULL_POINTER
+    lat.channels = 5
+    assert lib.nt_bc6_init(C.byref(lat), None) == abi.NT_ERR_UNSUPPORTED
+    lat = st.params().latents
+    lat.grids[0].width = 6
+    assert lib.nt_bc6_init(C.byref(lat), None) == abi.NT_ERR_INVALID_ARGUMENT
     with pytest.raises(nt.NtError) as e:
         nt.check(lib.nt_decode(None, None))
     assert e.value.status == abi.NT_ERR_NULL_POINTER

@@ -139,6 +139,8 @@ TRAIN_CASES = [
     ("c4", 128, (64, 32), (8, 8), abi.NT_UNCONSTRAINED),
     ("ref", 64, (32, 16), (0, 0), abi.NT_BLOCK_FEATURES),
     ("ref", 64, (32, 16), (5, 7), abi.NT_FINALIZE),
+    ("c2", 64, (32, 16), (3, 9), abi.NT_BLOCK_FEATURES),
+    ("c4", 128, (32, 16), (0, 0), abi.NT_FINALIZE),
 ]
 
 
@@ -233,6 +235,42 @@ def test_optimize_block_latents(lib, O):
     for g, gg in zip(st.grids, gs.grids):
         assert np.array_equal(to_np(gg.block_params), g.block_params)
         assert np.array_equal(to_np(gg.block_grads), g.block_grads)
+
+
+@pytest.mark.parametrize("C_,sizes", [(3, [(32, 6), (16, 5)]), (16, [(64, 7), (16, 3)]),
+                                      (8, [(8, 4)]), (4, [(4, 3), (12, 2)])])
+def test_bc6_init_bit_exact(lib, O, C_, sizes):
+    """nt_bc6_init == the oracle's block records, bit for bit, on every mip down to 1x1."""
+    import torch
+    say(f"case: bc6 init C={C_} grids={sizes}")
+    rng = np.random.default_rng(60 + C_)
+    grids = []
+    for size, mips in sizes:
+        g = P.make_grid(size, size, mips, C_, rng, blocks=True)
+        # Unconstrained latents as training leaves them: mostly positive, a few small
+        # negative texels and a run of equal texels.
+        g.values[:] = np.abs(rng.normal(0.3, 0.4, g.values.size)).astype(np.float32)
+        g.values[: 4 * C_] *= -1e-3
+        g.values[16 * C_: 32 * C_] = 0.125
+        g.block_params[:] = 0
+        grids.append(g)
+    lat = abi.nt_latents()
+    lat.num_grids, lat.channels = len(grids), C_
+    for i, g in enumerate(grids):
+        lat.grids[i] = g.struct()
+    assert O.ntref_bc6_init(C.byref(lat)) == 0
+    ggrids = [g.converted(True, "cuda") for g in grids]
+    for gg in ggrids:
+        gg.block_params.fill_(float("nan"))  # every record must be written
+    glat = abi.nt_latents()
+    glat.num_grids, glat.channels = len(ggrids), C_
+    for i, g in enumerate(ggrids):
+        glat.grids[i] = g.struct()
+    nt.check(lib.nt_bc6_init(C.byref(glat), None))
+    sync()
+    for g, gg in zip(grids, ggrids):
+        got = to_np(gg.block_params)
+        assert np.array_equal(got.view(np.uint32), g.block_params.view(np.uint32))
 
 
 # ---- inference (train.cu:917-961) --------------------------------------------------------------

@@ -86,3 +86,34 @@ def test_host_checkpoint_resume(program, tmp_path):
     a, b = _mse(full, "\nInference MSE"), _mse(resumed, "\nInference MSE")
     print(f"MSE uninterrupted {a:.6f}, resumed {b:.6f}", flush=True)
     assert abs(a - b) <= 0.02 * a
+
+
+@pytest.mark.gpu
+def test_host_phase_schedule(program, tmp_path):
+    """--phases 60,60 with --iters 150: unconstrained, then BC6 blocks initialised by
+    nt_bc6_init and trained, then network-only finalize; the saved image carries the block
+    records, every one with a valid partition, mode 0 and finite values."""
+    import numpy as np
+    from neural_textures_amd import model as M
+
+    ck = str(tmp_path / "phases.ntm")
+    cmd = [program, "--mode", "0", "--image", "256", "--iters", "150", "--progress", "50",
+           "--samples", "16384", "--grids", "2", "--channels", "16", "--hidden", "64,64",
+           "--targets", "9", "--feature-lr", "1e-2", "--network-lr", "5e-3",
+           "--phases", "60,60", "--save", ck]
+    print("running", " ".join(cmd), flush=True)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=110)
+    text = out.stdout + out.stderr
+    assert out.returncode == 0, text
+    assert "Completed iteration 150 / 150" in text
+    mse = _mse(text, "\nInference MSE")
+    assert mse == mse and mse < 1.0
+    m = M.load_model(ck)
+    assert m.step == 150 and m.contents & 4  # NT_MODEL_BLOCKS
+    for g in m.grids:
+        rec = g.block_params.reshape(-1, 4 * 16 + 18)
+        part = rec[:, 4 * 16 + 16].view(np.int32)
+        assert np.all((part >= 0) & (part < 32))
+        assert np.all(rec[:, 4 * 16 + 17].view(np.int32) == 0)
+        assert np.isfinite(rec[:, :4 * 16 + 16]).all()
+        assert np.abs(rec[:, :4 * 16]).max() > 0  # written by the init, then trained

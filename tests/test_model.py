@@ -44,7 +44,7 @@ def test_crc32c_check_value():
 
 
 def make_model(rng, state=True, codec=True, shapes=((20, 12, 3), (9, 9, 2)), channels=8,
-               sizes=(16, 32, 12), used=10, step=17):
+               sizes=(16, 32, 12), used=10, step=17, blocks=False):
     net = P.make_network(list(sizes), used_outputs=used, rng=rng)
     for l in range(net.num_layers):
         net.biases[l] = P.f16_bits(rng.normal(size=sizes[l + 1]))
@@ -60,16 +60,23 @@ def make_model(rng, state=True, codec=True, shapes=((20, 12, 3), (9, 9, 2)), cha
                                         rng.integers(0, 256, n, dtype=np.uint8)))
         if state:
             n = P.mip_chain_layout(w, h, mips)[1] * channels
-            m.grids.append(P.Grid(w, h, mips, channels,
-                                  values=rng.normal(size=n).astype(np.float32),
-                                  moment1=rng.normal(size=n).astype(np.float32),
-                                  moment2=rng.random(n).astype(np.float32)))
+            grid = P.Grid(w, h, mips, channels,
+                          values=rng.normal(size=n).astype(np.float32),
+                          moment1=rng.normal(size=n).astype(np.float32),
+                          moment2=rng.random(n).astype(np.float32))
+            if blocks:
+                nb = P.block_chain_layout(w, h, mips)[1]
+                grid.block_params = rng.normal(size=nb * (4 * channels + 18)).astype(np.float32)
+                grid.block_moment1 = rng.normal(size=nb * (4 * channels + 16)).astype(np.float32)
+                grid.block_moment2 = rng.random(nb * (4 * channels + 16)).astype(np.float32)
+            m.grids.append(grid)
     return m
 
 
 SECTION_TYPES = {1: "codec", 2: "weights", 3: "biases", 4: "latents", 5: "latent_moment1",
                  6: "latent_moment2", 7: "weight_moment1", 8: "weight_moment2",
-                 9: "bias_moment1", 10: "bias_moment2"}
+                 9: "bias_moment1", 10: "bias_moment2", 11: "block_params",
+                 12: "block_moment1", 13: "block_moment2"}
 
 
 def expected_sections(m: M.Model):
@@ -88,13 +95,19 @@ def expected_sections(m: M.Model):
             for t, a in ((7, m.net.weight_moment1[l]), (8, m.net.weight_moment2[l]),
                          (9, m.net.bias_moment1[l]), (10, m.net.bias_moment2[l])):
                 out.append((t, l, np.asarray(a, np.float32).tobytes()))
+    if m.contents & abi.NT_MODEL_BLOCKS:
+        for g, grid in enumerate(m.grids):
+            for t, a in ((11, grid.block_params), (12, grid.block_moment1), (13, grid.block_moment2)):
+                out.append((t, g, a.tobytes()))
     return out
 
 
-@pytest.mark.parametrize("state,codec", [(True, True), (True, False), (False, True)])
-def test_image_layout_read_back_independently(lib, state, codec):
-    rng = np.random.default_rng(3 + 2 * state + codec)
-    m = make_model(rng, state=state, codec=codec)
+@pytest.mark.parametrize("state,codec,blocks", [(True, True, False), (True, False, False),
+                                                (False, True, False), (True, True, True)])
+def test_image_layout_read_back_independently(lib, state, codec, blocks):
+    rng = np.random.default_rng(3 + 2 * state + codec + 4 * blocks)
+    shapes = ((20, 12, 3), (8, 8, 4)) if blocks else ((20, 12, 3), (9, 9, 2))
+    m = make_model(rng, state=state, codec=codec, blocks=blocks, shapes=shapes)
     img = M.model_image(m)
     raw = img.tobytes()
     magic, version, hbytes, nsec, contents, total, meta_crc = struct.unpack_from("<8s4IQI", raw, 0)
@@ -127,12 +140,12 @@ def test_image_layout_read_back_independently(lib, state, codec):
 
 def test_round_trip(lib, tmp_path):
     rng = np.random.default_rng(11)
-    m = make_model(rng)
+    m = make_model(rng, blocks=True, shapes=((20, 12, 3), (8, 8, 4)))
     path = str(tmp_path / "tex.ntm")
     n = M.save_model(path, m)
     assert n == (tmp_path / "tex.ntm").stat().st_size
     r = M.load_model(path)
-    assert (r.channels, r.shapes, r.step, r.contents) == (m.channels, m.shapes, 17, 3)
+    assert (r.channels, r.shapes, r.step, r.contents) == (m.channels, m.shapes, 17, 7)
     assert r.net.sizes == m.net.sizes and r.net.used_outputs == m.net.used_outputs
     for name in ("weights", "biases", "weight_moment1", "weight_moment2", "bias_moment1",
                  "bias_moment2"):
@@ -142,7 +155,8 @@ def test_round_trip(lib, tmp_path):
         assert (a.width, a.height, a.num_mips) == (b.width, b.height, b.num_mips)
         assert np.array_equal(a.blocks, b.blocks)
     for a, b in zip(r.grids, m.grids):
-        for name in ("values", "moment1", "moment2"):
+        for name in ("values", "moment1", "moment2", "block_params", "block_moment1",
+                     "block_moment2"):
             assert np.array_equal(getattr(a, name).view(np.uint32), getattr(b, name).view(np.uint32))
     # An image saved again from what was loaded is the same bytes.
     assert np.array_equal(M.model_image(r), M.read_image(path))
@@ -221,7 +235,8 @@ def test_rejects_bad_descriptions(lib):
     m = make_model(rng, channels=8)
     info = M._info(m)
     assert lib.nt_model_bytes(C.byref(info)) > 0
-    for field, value in [("contents", 0), ("contents", 4), ("num_grids", 0), ("num_grids", 5),
+    for field, value in [("contents", 0), ("contents", 4), ("contents", 8), ("num_grids", 0),
+                         ("num_grids", 5),
                          ("channels", 0), ("channels", 17), ("num_layers", 0), ("num_layers", 7),
                          ("used_outputs", 13), ("step", -1)]:
         bad = M._info(m)
@@ -237,6 +252,9 @@ def test_rejects_bad_descriptions(lib):
     assert lib.nt_model_bytes(C.byref(bad)) == 0
     bad = M._info(m)
     bad.width[1] = 0
+    assert lib.nt_model_bytes(C.byref(bad)) == 0
+    bad = M._info(m)  # block records need sizes that are multiples of 4 (9 is not)
+    bad.contents |= abi.NT_MODEL_BLOCKS
     assert lib.nt_model_bytes(C.byref(bad)) == 0
     bad = M._info(m)
     bad.sizes[1] = 1025
