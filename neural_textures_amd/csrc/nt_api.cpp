@@ -253,7 +253,7 @@ int pack_targets(const nt_texture *tex, int ntex, int8_t *out_tex, int8_t *out_c
 }
 
 struct TrainPlan {
-    int shape, nwg, chunks_per_wg, tiles_x, P, stage1_blocks, rows_per_block;
+    int shape, nwg, chunks_per_wg, tiles_x, P;
     int fp_floats, fp_stride, tile_ok, scatter_mfma, scatter_split, scatter_off, w_rows, union_off;
     int vbox_floats, vbox_off;
     size_t weight_bytes;
@@ -369,9 +369,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->lds = lds;
     plan->nwg = d.nwg;
     plan->rows = d.nwg; // the groups of a workgroup merge their partials in LDS
-    plan->stage1_blocks = (plan->rows + plan->rows_per_block - 1) / plan->rows_per_block;
-    plan->workspace = plan->weight_bytes +
-                      ((size_t)plan->rows + (size_t)plan->stage1_blocks) * (size_t)plan->P * sizeof(float);
+    plan->workspace = plan->weight_bytes + (size_t)plan->rows * (size_t)plan->P * sizeof(float);
     d.image_w = p->image_width;
     d.image_h = p->image_height;
     d.off_x = p->texel_offset_x;
@@ -415,11 +413,8 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         return fail(NT_ERR_INVALID_ARGUMENT, "too many samples");
     plan->nwg = plan->tiles_x * tiles_y;
     plan->P = train_grad_total(shape);
-    plan->rows_per_block = 32;
-    plan->stage1_blocks = (plan->nwg + plan->rows_per_block - 1) / plan->rows_per_block;
     plan->weight_bytes = train_weight_bytes(shape);
-    plan->workspace = plan->weight_bytes +
-                      ((size_t)plan->nwg + (size_t)plan->stage1_blocks) * (size_t)plan->P * sizeof(float);
+    plan->workspace = plan->weight_bytes + (size_t)plan->nwg * (size_t)plan->P * sizeof(float);
 
     // LDS footprint box per grid: every texel a 64 x 8 block of positions can touch (the
     // bilinear corners of positions in [x, x + 64] span at most ceil(64 r) + 2 texels, plus
@@ -688,11 +683,8 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
 
     ReduceDesc r{};
     r.partial = partial;
-    r.tmp = partial + (size_t)plan.rows * plan.P;
     r.rows = plan.rows;
-    r.rows_per_block = plan.rows_per_block;
     r.P = plan.P;
-    r.stage1_blocks = plan.stage1_blocks;
     r.num_layers = p->mlp.num_layers;
     int off = 0;
     for (int l = 0; l < p->mlp.num_layers; ++l) {

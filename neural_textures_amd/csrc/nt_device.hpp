@@ -88,6 +88,29 @@ __device__ __forceinline__ T *sreg(T *p)
     return (T *)(((uint64_t)hi << 32) | lo);
 }
 
+// A pointer into global memory, for loads through pointers whose address space the compiler
+// cannot infer (sreg() round-trips them through integers): such loads would otherwise be
+// flat_load, which also counts in lgkmcnt, so every wait for an LDS access would wait for
+// them too. global_load counts in vmcnt only.
+template <class T>
+using global_ptr = const __attribute__((address_space(1))) T *;
+template <int N>
+struct RawWords {
+    using type = __attribute__((ext_vector_type(N))) unsigned int;
+};
+template <>
+struct RawWords<1> {
+    using type = unsigned int;
+};
+// Load a 4-, 8- or 16-byte value from global memory.
+template <class T>
+__device__ __forceinline__ T load_global(const T *p)
+{
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 16, "4, 8 or 16 bytes");
+    using V = typename RawWords<sizeof(T) / 4>::type;
+    return __builtin_bit_cast(T, *(global_ptr<V>)p);
+}
+
 __device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)bits_h(b); }

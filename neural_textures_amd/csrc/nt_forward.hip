@@ -202,9 +202,9 @@ __device__ __forceinline__ void codec_texel16(const uint8_t *base, int bw, int t
 {
     const uint8_t *rec = base + ((int64_t)(ty >> 2) * bw + (tx >> 2)) * (12 * 16);
     const int pix = ((ty & 3) << 2) + (tx & 3);
-    const uint4 e0 = *(const uint4 *)rec, e1 = *(const uint4 *)(rec + 16);
-    const uint4 e2 = *(const uint4 *)(rec + 32), e3 = *(const uint4 *)(rec + 48);
-    const uint2 ix = *(const uint2 *)(rec + 64 + pix * 8);
+    const uint4 *r4 = (const uint4 *)rec;
+    const uint4 e0 = load_global(r4), e1 = load_global(r4 + 1), e2 = load_global(r4 + 2), e3 = load_global(r4 + 3);
+    const uint2 ix = load_global((const uint2 *)(rec + 64 + pix * 8));
     const uint32_t ends[16] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w,
                                e2.x, e2.y, e2.z, e2.w, e3.x, e3.y, e3.z, e3.w};
 #pragma unroll
@@ -241,10 +241,10 @@ __device__ __forceinline__ void sample_decode16(const FwdDesc &d, const int64_t 
             h8 v0l, v0h, v1l, v1h, v2l, v2h, v3l, v3h;
             if constexpr (EXPANDED) {
                 const uint4 *t = (const uint4 *)(hv + off * 16);
-                const uint4 a0 = t[2 * (y0 * w + x0)], a1 = t[2 * (y0 * w + x0) + 1];
-                const uint4 b0 = t[2 * (y0 * w + x1)], b1 = t[2 * (y0 * w + x1) + 1];
-                const uint4 c0 = t[2 * (y1 * w + x0)], c1 = t[2 * (y1 * w + x0) + 1];
-                const uint4 e0 = t[2 * (y1 * w + x1)], e1 = t[2 * (y1 * w + x1) + 1];
+                const uint4 a0 = load_global(t + 2 * (y0 * w + x0)), a1 = load_global(t + 2 * (y0 * w + x0) + 1);
+                const uint4 b0 = load_global(t + 2 * (y0 * w + x1)), b1 = load_global(t + 2 * (y0 * w + x1) + 1);
+                const uint4 c0 = load_global(t + 2 * (y1 * w + x0)), c1 = load_global(t + 2 * (y1 * w + x0) + 1);
+                const uint4 e0 = load_global(t + 2 * (y1 * w + x1)), e1 = load_global(t + 2 * (y1 * w + x1) + 1);
                 v0l = __builtin_bit_cast(h8, a0), v0h = __builtin_bit_cast(h8, a1);
                 v1l = __builtin_bit_cast(h8, b0), v1h = __builtin_bit_cast(h8, b1);
                 v2l = __builtin_bit_cast(h8, c0), v2h = __builtin_bit_cast(h8, c1);

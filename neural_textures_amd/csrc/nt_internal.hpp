@@ -117,8 +117,7 @@ struct PrepDesc {
 // Gradient reduction descriptor: partial[rows][P] -> mlp gradients.
 struct ReduceDesc {
     const float *partial;
-    float *tmp;
-    int rows, rows_per_block, P, stage1_blocks;
+    int rows, P;
     int num_layers;
     int off[NT_MAX_LAYERS], kin[NT_MAX_LAYERS], kout[NT_MAX_LAYERS], nbias[NT_MAX_LAYERS];
     float *wgrad[NT_MAX_LAYERS];

@@ -182,20 +182,23 @@ __device__ __forceinline__ void layer_forward(const h8 *frags, const float *bias
     }
 }
 
-// D tiles -> chained fp16 fragments, with optional ReLU (mlp.h:35-38).
+// D tiles -> chained fp16 fragments, with optional ReLU (mlp.h:35-38). The ReLU is taken
+// after the conversion, as a signed 16-bit max with 0 on the pair (v_pk_max_i16): negative
+// halves and -0 have the sign bit set, so they become +0. fp16 rounding is monotone, so
+// this equals rounding max(x, 0), in one instruction per pair instead of a float max (and
+// its NaN canonicalisation) per element.
 template <int NQ, int NA, bool RELU>
 __device__ __forceinline__ void to_fragments(const f16v (&acc)[NA], h8 (&y)[NQ])
 {
+    typedef short s2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            f2 v = {acc[q >> 1][8 * (q & 1) + e], acc[q >> 1][8 * (q & 1) + e + 1]};
-            if (RELU) {
-                v[0] = v[0] > 0.f ? v[0] : 0.f;
-                v[1] = v[1] > 0.f ? v[1] : 0.f;
-            }
-            const h2 h = __builtin_convertvector(v, h2); // v_cvt_pk_f16_f32
+            const f2 v = {acc[q >> 1][8 * (q & 1) + e], acc[q >> 1][8 * (q & 1) + e + 1]};
+            h2 h = __builtin_convertvector(v, h2); // v_cvt_pk_f16_f32
+            if (RELU)
+                h = __builtin_bit_cast(h2, __builtin_elementwise_max(__builtin_bit_cast(s2, h), (s2)0));
             y[q][e] = h[0];
             y[q][e + 1] = h[1];
         }

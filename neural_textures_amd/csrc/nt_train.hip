@@ -103,7 +103,7 @@ __device__ __forceinline__ void gather_unconstrained(const TrainDesc &d, const S
                     const int tx = wrap_near(x0 + (c & 1), gw);
                     const int ty = wrap_near(y0 + (c >> 1), gh);
                     const float4 *p = (const float4 *)(vals + ((int64_t)ty * gw + tx) * C + cb);
-                    acc = accumulate_products(acc, w[c], p[0], p[1]);
+                    acc = accumulate_products(acc, w[c], load_global(p), load_global(p + 1));
                 }
             }
         } else {
@@ -150,7 +150,7 @@ __device__ __forceinline__ void load_value_box(const TrainDesc &d, float4 *vbox,
             const int texel = i >> 2, part = i & 3;
             const int lx = texel % gr.fp_w, ly = texel / gr.fp_w;
             const int gx = wrap_coord(flo_x[gi] + lx, gr.w), gy = wrap_coord(flo_y[gi] + ly, gr.h);
-            dst[i] = ((const float4 *)(gr.values + ((int64_t)gy * gr.w + gx) * 16))[part];
+            dst[i] = load_global((const float4 *)(gr.values + ((int64_t)gy * gr.w + gx) * 16) + part);
         }
     }
 }
@@ -185,8 +185,8 @@ __device__ __forceinline__ void gather_box16(const TrainDesc &d, const SampleFoo
                     const float4 *p = (const float4 *)(gr.values +
                                                        ((int64_t)wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w)) * 16 +
                                                        8 * g);
-                    a = p[0];
-                    b = p[1];
+                    a = load_global(p);
+                    b = load_global(p + 1);
                 }
                 acc = accumulate_products(acc, f.w[q][c], a, b);
             }
@@ -889,45 +889,44 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 
 // Two-stage deterministic reduction of the per-workgroup partials into the network
 // gradients (which the contract says are accumulated into, train.cu:1028-1048).
-__global__ __launch_bounds__(256) void reduce_stage1(ReduceDesc d)
+// partial[rows][P] -> the MLP gradients, in one pass and a fixed order: a workgroup owns 64
+// parameters; wave w sums rows [w R/4, (w+1) R/4) in row order over four interleaved
+// accumulators, and the four wave sums are added in wave order. The same bits on every run.
+__global__ __launch_bounds__(256) void reduce_rows(ReduceDesc d)
 {
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= d.P)
-        return;
-    const int r0 = blockIdx.y * d.rows_per_block;
-    const int r1 = min(r0 + d.rows_per_block, d.rows);
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int p = blockIdx.x * 64 + lane;
+    const int per = (d.rows + 3) / 4;
+    const int r0 = wave * per, r1 = min(r0 + per, d.rows);
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-    int r = r0;
-    for (; r + 4 <= r1; r += 4) {
-        s0 += d.partial[(int64_t)r * d.P + p];
-        s1 += d.partial[(int64_t)(r + 1) * d.P + p];
-        s2 += d.partial[(int64_t)(r + 2) * d.P + p];
-        s3 += d.partial[(int64_t)(r + 3) * d.P + p];
+    if (p < d.P) {
+        const float *col = d.partial + p;
+        int r = r0;
+        for (; r + 4 <= r1; r += 4) {
+            s0 += col[(int64_t)r * d.P];
+            s1 += col[(int64_t)(r + 1) * d.P];
+            s2 += col[(int64_t)(r + 2) * d.P];
+            s3 += col[(int64_t)(r + 3) * d.P];
+        }
+        for (; r < r1; ++r)
+            s0 += col[(int64_t)r * d.P];
     }
-    for (; r < r1; ++r)
-        s0 += d.partial[(int64_t)r * d.P + p];
-    d.tmp[(int64_t)blockIdx.y * d.P + p] = (s0 + s1) + (s2 + s3);
-}
-
-__global__ __launch_bounds__(256) void reduce_stage2(ReduceDesc d)
-{
-    const int p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= d.P)
+    part[wave][lane] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (wave != 0 || p >= d.P)
         return;
-    float s = 0.f;
-    for (int r = 0; r < d.stage1_blocks; ++r)
-        s += d.tmp[(int64_t)r * d.P + p];
+    const float s = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
     int l = 0;
     for (int k = 1; k < d.num_layers; ++k)
         if (p >= d.off[k])
             l = k;
     const int local = p - d.off[l];
     const int nw = d.kin[l] * d.kout[l];
-    if (local < nw) {
+    if (local < nw)
         d.wgrad[l][local] += s;
-    } else if (local - nw < d.nbias[l]) {
+    else if (local - nw < d.nbias[l])
         d.bgrad[l][local - nw] += s;
-    }
 }
 
 // Weight fragments and fp32 biases in the train kernel's LDS order, computed once per step
@@ -954,9 +953,7 @@ static hipError_t launch_prep(const PrepDesc &d, hipStream_t s)
 
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s)
 {
-    dim3 g1((d.P + 255) / 256, d.stage1_blocks);
-    hipLaunchKernelGGL(reduce_stage1, g1, dim3(256), 0, s, d);
-    hipLaunchKernelGGL(reduce_stage2, dim3((d.P + 255) / 256), dim3(256), 0, s, d);
+    hipLaunchKernelGGL(reduce_rows, dim3((d.P + 63) / 64), dim3(256), 0, s, d);
     return hipGetLastError();
 }
 

@@ -179,7 +179,7 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
                     const int y = wrap_coord(gy0 + jj, d.image_h);
                     for (int i = 0; i < 4; ++i) {
                         const int x = wrap_coord(gx0 + i, d.image_w);
-                        const float4 p = *(const float4 *)(tex + ((int64_t)y * d.image_w + x) * 4);
+                        const float4 p = load_global((const float4 *)(tex + ((int64_t)y * d.image_w + x) * 4));
                         const float wxy = wx[i] * wy[jj];
                         acc[0] = fmaf(p.x, wxy, acc[0]);
                         acc[1] = fmaf(p.y, wxy, acc[1]);
@@ -224,7 +224,7 @@ __device__ __forceinline__ void gather16(const Train16Desc &d, float u, float v,
             const float4 *p = (const float4 *)(vals + ((int64_t)ty * w + tx) * 16);
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                t[c][k] = p[k];
+                t[c][k] = load_global(p + k);
         }
         h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
 #pragma unroll
