@@ -1047,6 +1047,71 @@ static size_t decode_workspace_layout(const nt_decode_params *p, size_t *seg_off
     return off;
 }
 
+// LDS boxes of the staged decode: for every grid the mips its pixels can sample (z ranges
+// over [mip_min, mip_max] as the kernel computes it), and for each the largest box any
+// block needs (footprint origins of a block's lowest and highest sample positions, plus the
+// bilinear neighbour). False when the boxes exceed kBoxMaxBytes.
+static bool plan_decode_box(const nt_decode_params *p, const FwdDesc &fd, int shape, DecodeBoxDesc *b)
+{
+    *b = DecodeBoxDesc{};
+    b->mlp = fd.mlp;
+    b->G = p->num_grids;
+    b->image_w = p->out_width;
+    b->image_h = p->out_height;
+    b->blocks_x = (p->out_width + kBoxBlockW - 1) / kBoxBlockW;
+    b->blocks_y = (p->out_height + kBoxBlockH - 1) / kBoxBlockH;
+    b->out16 = p->output;
+    b->out_stride = fd.out_stride;
+    b->seed = p->seed;
+    b->jitter = p->jitter;
+    b->mip_min = p->mip_min;
+    b->mip_max = p->mip_max;
+    const float dz = p->mip_max - p->mip_min;
+    const float za = fmaf(dz, 0.f, p->mip_min), zb = fmaf(dz, 1.f - 0x1p-24f, p->mip_min);
+    const float zlo = std::min(za, zb), zhi = std::max(za, zb);
+    if (!std::isfinite(zlo) || !std::isfinite(zhi) || !std::isfinite(p->jitter))
+        return false;
+    int texels = 0;
+    for (int gi = 0; gi < p->num_grids; ++gi) {
+        BoxGrid &q = b->grid[gi];
+        q.texels = fd.half_values[gi];
+        q.w = fd.grid[gi].w;
+        q.h = fd.grid[gi].h;
+        q.num_mips = fd.grid[gi].num_mips;
+        for (int m = 0; m < NT_MAX_MIPS; ++m)
+            q.mip_off[m] = fd.grid[gi].mip_off[m];
+        const int top = q.num_mips - 1;
+        const float fl = floorf(zlo), fh = floorf(zhi);
+        q.mip_lo = (int)std::min(std::max(fl, 0.f), (float)top);
+        q.mip_hi = (int)std::min(std::max(fh + (zhi > fh ? 1.f : 0.f), 0.f), (float)top);
+        for (int m = q.mip_lo; m <= q.mip_hi; ++m) {
+            const int w = mip_dim_h(q.w, m), h = mip_dim_h(q.h, m);
+            int bw = 2, bh = 2;
+            for (int bx = 0; bx < b->blocks_x; ++bx) {
+                const int x0 = bx * kBoxBlockW, x1 = std::min(x0 + kBoxBlockW, p->out_width) - 1;
+                bw = std::max(bw, box_last(x1, p->out_width, p->jitter, w) -
+                                      box_origin(x0, p->out_width, p->jitter, w) + 2);
+            }
+            for (int by = 0; by < b->blocks_y; ++by) {
+                const int y0 = by * kBoxBlockH, y1 = std::min(y0 + kBoxBlockH, p->out_height) - 1;
+                bh = std::max(bh, box_last(y1, p->out_height, p->jitter, h) -
+                                      box_origin(y0, p->out_height, p->jitter, h) + 2);
+            }
+            if (bw > 0xFFFF || bh > 0x7FFF || (int64_t)bw * bh * 32 > kBoxMaxBytes)
+                return false;
+            q.box_w[m] = bw;
+            q.box_h[m] = bh;
+            q.box_off[m] = texels;
+            texels += bw * bh;
+            if ((int64_t)texels * 32 > kBoxMaxBytes)
+                return false;
+        }
+    }
+    b->box_texels = texels;
+    b->lds_box_off = (int)((decode_box_weight_bytes(shape) + 15) & ~(size_t)15);
+    return b->lds_box_off > 0;
+}
+
 size_t nt_decode_workspace_bytes(const nt_decode_params *p)
 {
     if (!p || p->channels != 16 || p->num_grids < 1 || p->num_grids > NT_MAX_GRIDS) {
@@ -1145,6 +1210,11 @@ int nt_decode(const nt_decode_params *p, void *stream)
         hipError_t e = launch_codec_expand(x, s);
         if (e != hipSuccess)
             return hip_status(e, "decode expand launch");
+        DecodeBoxDesc b;
+        if (plan_decode_box(p, d, shape, &b)) {
+            ProfileScope prof(s);
+            return hip_status(launch_decode_box(shape, b, s), "decode launch");
+        }
         ProfileScope prof(s);
         return hip_status(launch_forward(shape, kFwdDecode16, d, s), "decode launch");
     }

@@ -434,13 +434,15 @@ __global__ __launch_bounds__(kFwdThreads, fwd_min_blocks<MODE>()) void forward_k
             // Lane group g holds output rows 4g .. 4g+3 and 8+4g .. 8+4g+3: with a row stride
             // that is a multiple of 4 each run of four is one 8-byte store.
             uint16_t *orow = d.out16 + (int64_t)s * d.out_stride;
+            const bool quads = (d.out_stride & 3) == 0; // uniform: one of the two paths runs
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int o = 8 * j + 4 * g;
                 const f2 v0 = {out[0][4 * j], out[0][4 * j + 1]}, v1 = {out[0][4 * j + 2], out[0][4 * j + 3]};
                 const h2 h0 = __builtin_convertvector(v0, h2), h1 = __builtin_convertvector(v1, h2);
-                if ((d.out_stride & 3) == 0 && o + 3 < d.out_stride) {
-                    *(uint2 *)(orow + o) = make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
+                if (quads) {
+                    if (o < d.out_stride)
+                        *(uint2 *)(orow + o) = make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
                 } else {
                     const _Float16 hv[4] = {h0[0], h0[1], h1[0], h1[1]};
 #pragma unroll
@@ -488,6 +490,202 @@ hipError_t launch_sse_reduce(const float *partial, int n, float *sse, hipStream_
 {
     hipLaunchKernelGGL(sse_reduce_kernel, dim3(1), dim3(256), 0, s, partial, n, sse);
     return hipGetLastError();
+}
+
+// ---- LDS-staged decode (second pass of the two-pass decode) ----------------------------
+// Same per-pixel arithmetic as forward_kernel<..., Decode16> (and so the same bits): the
+// corner texels come from per-block LDS boxes instead of HBM/L2. Box entry of (grid, mip):
+// {first texel, width | height << 16, origin x, origin y}.
+
+__device__ __forceinline__ int wrap_mod(int c, int size)
+{
+    const int r = c % size;
+    return r < 0 ? r + size : r;
+}
+
+template <int G>
+__device__ __forceinline__ void sample_box16(const int4 *gtab, const int4 *tab, const uint4 *box, float u,
+                                             float v, float z, int g, h8 (&x)[G])
+{
+#pragma unroll
+    for (int j = 0; j < G / 2; ++j) {
+        const int gi = 2 * j + g;
+        // Grid sizes from LDS (per tile) rather than kernel arguments kept live across the loop.
+        const int4 gp = gtab[gi];
+        const int gw = gp.x, gh = gp.y, nmips = gp.z;
+        int mips[2];
+        float mw[2];
+        const int nm = mip_pair(nmips, z, mips, mw);
+        h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
+        for (int mi = 0; mi < nm; ++mi) {
+            const int w = mip_dim(gw, mips[mi]), h = mip_dim(gh, mips[mi]);
+            const Footprint f = bilinear_footprint(u, v, w, h, mw[mi]);
+            const int4 e = tab[gi * NT_MAX_MIPS + mips[mi]];
+            const int bw = e.y & 0xFFFF, bh = e.y >> 16;
+            // In the box by construction; the clamps only guard LDS addressing.
+            const int lx = min(max(f.x0 - e.z, 0), bw - 2), ly = min(max(f.y0 - e.w, 0), bh - 2);
+            const uint4 *t = box + 2 * (e.x + ly * bw + lx);
+            const int row = 2 * bw;
+            fma_corner16(lo, hi, f.w[0], __builtin_bit_cast(h8, t[0]), __builtin_bit_cast(h8, t[1]));
+            fma_corner16(lo, hi, f.w[1], __builtin_bit_cast(h8, t[2]), __builtin_bit_cast(h8, t[3]));
+            fma_corner16(lo, hi, f.w[2], __builtin_bit_cast(h8, t[row]), __builtin_bit_cast(h8, t[row + 1]));
+            fma_corner16(lo, hi, f.w[3], __builtin_bit_cast(h8, t[row + 2]), __builtin_bit_cast(h8, t[row + 3]));
+            // One mip level's reads at a time keeps the wave within 128 VGPRs.
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        x[2 * j] = lo;
+        x[2 * j + 1] = hi;
+    }
+}
+
+template <class S>
+__global__ __launch_bounds__(kFwdThreads, 3) void decode_box_kernel(DecodeBoxDesc d)
+{
+    using LY = FwdLayout<S>;
+    constexpr int L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
+    constexpr int kTiles = kBoxBlockW / 32 * kBoxBlockH;
+    extern __shared__ __align__(16) unsigned char smem[];
+    h8 *frags = (h8 *)smem;
+    float *bias = (float *)(smem + LY::bias_off);
+    uint4 *box = (uint4 *)(smem + d.lds_box_off);
+    __shared__ int4 tab[NT_MAX_GRIDS * NT_MAX_MIPS];
+    __shared__ int4 gtab[NT_MAX_GRIDS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
+    stage_weights<S, true, true>(d.mlp, frags, bias, tid, kFwdThreads);
+    if (tid < NT_MAX_GRIDS)
+        gtab[tid] = tid < d.G ? make_int4(d.grid[tid].w, d.grid[tid].h, d.grid[tid].num_mips, 0) : make_int4(1, 1, 1, 0);
+
+    const int nblocks = d.blocks_x * d.blocks_y;
+    for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+        const int bx0 = (blk % d.blocks_x) * kBoxBlockW, by0 = (blk / d.blocks_x) * kBoxBlockH;
+        __syncthreads(); // the previous block's reads of the boxes (and the weight staging) are done
+        if (tid < NT_MAX_GRIDS * NT_MAX_MIPS) {
+            const int gi = tid / NT_MAX_MIPS, m = tid % NT_MAX_MIPS;
+            int4 e = make_int4(0, 0x20002, 0, 0);
+            if (gi < d.G) {
+                const BoxGrid &q = d.grid[gi];
+                if (m >= q.mip_lo && m <= q.mip_hi) {
+                    e.x = q.box_off[m];
+                    e.y = q.box_w[m] | (q.box_h[m] << 16);
+                    e.z = box_origin(bx0, d.image_w, d.jitter, mip_dim(q.w, m));
+                    e.w = box_origin(by0, d.image_h, d.jitter, mip_dim(q.h, m));
+                }
+            }
+            tab[tid] = e;
+        }
+        __syncthreads();
+        // Stage the boxes: texel k of box (gi, m) is global texel (origin + (k % bw, k / bw)),
+        // wrapped; two 16-byte halves per texel.
+        for (int i = tid; i < 2 * d.box_texels; i += kFwdThreads) {
+            const int k = i >> 1;
+            int gi = 0, m = 0;
+            for (int a = 0; a < d.G; ++a) {
+                const BoxGrid &q = d.grid[a];
+                for (int b = q.mip_lo; b <= q.mip_hi; ++b)
+                    if (k >= q.box_off[b]) {
+                        gi = a;
+                        m = b;
+                    }
+            }
+            const BoxGrid &q = d.grid[gi];
+            const int4 e = tab[gi * NT_MAX_MIPS + m];
+            const int bw = e.y & 0xFFFF, local = k - e.x;
+            const int w = mip_dim(q.w, m), h = mip_dim(q.h, m);
+            const int gx = wrap_mod(e.z + local % bw, w), gy = wrap_mod(e.w + local / bw, h);
+            const uint4 *src = (const uint4 *)(q.texels + (q.mip_off[m] + (int64_t)gy * w + gx) * 16);
+            box[i] = load_global(src + (i & 1));
+        }
+        __syncthreads();
+
+        for (int t = wave; t < kTiles; t += kFwdWaves) {
+            const int px = bx0 + 32 * (t % (kBoxBlockW / 32)) + c, py = by0 + t / (kBoxBlockW / 32);
+            const bool valid = px < d.image_w && py < d.image_h;
+            const int cx = min(px, d.image_w - 1), cy = min(py, d.image_h - 1);
+            const int s = cy * d.image_w + cx;
+            // Position and mip as forward_kernel<..., Decode16> (pixel index s).
+            uint32_t st = mix_seed((uint32_t)s, d.seed);
+            const float jx = uniform01(st) - 0.5f;
+            const float jy = uniform01(st) - 0.5f;
+            const float zu = uniform01(st);
+            const float posx = clampf(fmaf(d.jitter, jx, (float)cx + 0.5f), 0.5f, (float)d.image_w - 0.5f);
+            const float posy = clampf(fmaf(d.jitter, jy, (float)cy + 0.5f), 0.5f, (float)d.image_h - 0.5f);
+            const float u = posx / (float)d.image_w;
+            const float v = posy / (float)d.image_h;
+            const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
+            h8 x0[KQ0];
+            sample_box16<KQ0>(gtab, tab, box, u, v, z, g, x0);
+
+            h8 xh[HQ];
+            {
+                f16v acc[HA];
+                layer_forward<KQ0, HA>(frags + S::fwd_off(0) * kWave, bias + S::bias_off(0), x0, acc, lane);
+                to_fragments<HQ, HA, true>(acc, xh);
+#pragma unroll
+                for (int l = 1; l < NH; ++l) {
+                    layer_forward<HQ, HA>(frags + S::fwd_off(l) * kWave, bias + S::bias_off(l), xh, acc, lane);
+                    to_fragments<HQ, HA, true>(acc, xh);
+                }
+            }
+            f16v out[1];
+            layer_forward<HQ, 1>(frags + S::fwd_off(L - 1) * kWave, bias + S::bias_off(L - 1), xh, out, lane);
+            if (!valid)
+                continue;
+            uint16_t *orow = d.out16 + (int64_t)s * d.out_stride;
+            const bool quads = (d.out_stride & 3) == 0;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int o = 8 * j + 4 * g;
+                const f2 v0 = {out[0][4 * j], out[0][4 * j + 1]}, v1 = {out[0][4 * j + 2], out[0][4 * j + 3]};
+                const h2 h0 = __builtin_convertvector(v0, h2), h1 = __builtin_convertvector(v1, h2);
+                if (quads) {
+                    if (o < d.out_stride)
+                        *(uint2 *)(orow + o) = make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
+                } else {
+                    const _Float16 hv[4] = {h0[0], h0[1], h1[0], h1[1]};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (o + r < d.out_stride)
+                            orow[o + r] = h_bits(hv[r]);
+                }
+            }
+        }
+    }
+}
+
+template <class S>
+static hipError_t launch_box(const DecodeBoxDesc &d, hipStream_t s)
+{
+    const int nblocks = d.blocks_x * d.blocks_y;
+    const int grid = nblocks < 2048 ? nblocks : 2048;
+    const size_t lds = (size_t)d.lds_box_off + (size_t)d.box_texels * 32;
+    if ((size_t)d.lds_box_off < FwdLayout<S>::bytes)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(decode_box_kernel<S>, dim3(grid), dim3(kFwdThreads), lds, s, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_box(int shape, const DecodeBoxDesc &d, hipStream_t s)
+{
+    switch (shape) {
+    case kShapeC2:
+        return launch_box<Shape<32, 64, 2>>(d, s);
+    case kShapeC4:
+        return launch_box<Shape<64, 64, 3>>(d, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+size_t decode_box_weight_bytes(int shape)
+{
+    switch (shape) {
+    case kShapeC2:
+        return FwdLayout<Shape<32, 64, 2>>::bytes;
+    case kShapeC4:
+        return FwdLayout<Shape<64, 64, 3>>::bytes;
+    default:
+        return 0;
+    }
 }
 
 template <class S, int C, int MODE>

@@ -159,6 +159,32 @@ struct Bc6InitDesc {
     int64_t start[kMaxExpandLevels + 1];
 };
 
+// Second pass of the two-pass decode, LDS-staged: a workgroup decodes blocks of
+// kBoxBlockW x kBoxBlockH output pixels; for every (grid, mip) the pixels of a block can
+// sample it first copies a box of expanded fp16 texels into LDS, then every pixel reads
+// its corners from there.
+constexpr int kBoxBlockW = 64;
+constexpr int kBoxBlockH = 16;
+constexpr int kBoxMaxBytes = 32 * 1024;
+struct BoxGrid {
+    const uint16_t *texels; // expanded fp16 mip chain, [texel][16]
+    int w, h, num_mips, mip_lo, mip_hi;
+    int box_w[NT_MAX_MIPS], box_h[NT_MAX_MIPS], box_off[NT_MAX_MIPS]; // LDS boxes, texels
+    int64_t mip_off[NT_MAX_MIPS];
+};
+struct DecodeBoxDesc {
+    MlpDesc mlp;
+    BoxGrid grid[NT_MAX_GRIDS];
+    int G;
+    int image_w, image_h, blocks_x, blocks_y;
+    int box_texels;  // all boxes, 32 bytes each
+    int lds_box_off; // byte offset of the boxes in dynamic LDS
+    uint16_t *out16;
+    int out_stride;
+    uint32_t seed;
+    float jitter, mip_min, mip_max;
+};
+
 // Forward-only passes: 256-thread workgroups (four waves) striding over 32-sample tiles,
 // at most kFwdMaxBlocks of them.
 constexpr int kFwdThreads = 256;
@@ -251,6 +277,25 @@ hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream
 int train_grad_total(int shape);
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s);
 hipError_t launch_forward(int shape, int mode, const FwdDesc &d, hipStream_t s);
+// Box origin (first texel) along one axis for the pixels [b0, ...) of a block: the
+// footprint origin of their lowest possible sample position (jitter at its extreme).
+__host__ __device__ inline int box_origin(int b0, int image, float jitter, int level)
+{
+    const float jmin = jitter >= 0.f ? -0.5f : 0.5f - 0x1p-24f;
+    float pos = fmaf(jitter, jmin, (float)b0 + 0.5f);
+    pos = pos < 0.5f ? 0.5f : (pos > (float)image - 0.5f ? (float)image - 0.5f : pos);
+    return (int)floorf(fmaf(pos / (float)image, (float)level, -0.5f));
+}
+// The footprint origin of the highest possible sample position of pixel b1.
+__host__ __device__ inline int box_last(int b1, int image, float jitter, int level)
+{
+    const float jmax = jitter >= 0.f ? 0.5f - 0x1p-24f : -0.5f;
+    float pos = fmaf(jitter, jmax, (float)b1 + 0.5f);
+    pos = pos < 0.5f ? 0.5f : (pos > (float)image - 0.5f ? (float)image - 0.5f : pos);
+    return (int)floorf(fmaf(pos / (float)image, (float)level, -0.5f));
+}
+hipError_t launch_decode_box(int shape, const DecodeBoxDesc &d, hipStream_t s);
+size_t decode_box_weight_bytes(int shape);
 // *sse += the sum of partial[0..n) in a fixed order (one workgroup).
 hipError_t launch_sse_reduce(const float *partial, int n, float *sse, hipStream_t s);
 hipError_t launch_net_adam(const NetAdamDesc &d, hipStream_t s);

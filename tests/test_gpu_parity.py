@@ -352,9 +352,14 @@ def test_codec_bit_exact(lib, O, w, h, c):
 
 # ---- decode from quantized latents ------------------------------------------------------------------
 
-def test_decode_from_codec_latents(lib, O):
+@pytest.mark.parametrize("W,H,jitter,mip_min,mip_max", [
+    (96, 96, 1.0, 0.0, 3.0),
+    (100, 37, -1.5, 0.5, 6.0),   # ragged blocks, negative jitter, mips past the last one
+    (70, 20, 3.0, -1.0, 1.0),    # negative mip coordinates clamp to mip 0
+], ids=["96x96", "100x37", "70x20"])
+def test_decode_from_codec_latents(lib, O, W, H, jitter, mip_min, mip_max):
     import torch
-    say("case: decode c4")
+    say(f"case: decode c4 {W}x{H} jitter {jitter} z [{mip_min}, {mip_max})")
     rng = np.random.default_rng(50)
     C16 = 16
     sizes = [(64, 5), (32, 5), (16, 4), (8, 3)]
@@ -370,7 +375,6 @@ def test_decode_from_codec_latents(lib, O):
             blob[offs[m]:offs[m] + blk.size] = blk
         blobs.append((size, mips, offs, blob))
     net = P.make_network([64, 64, 64, 64, 12], rng=rng, init="xavier")
-    W = H = 96
 
     def dparams(blob_ptrs, netv, out_ptr):
         d = abi.nt_decode_params()
@@ -383,7 +387,7 @@ def test_decode_from_codec_latents(lib, O):
             d.grids[i].blocks = blob_ptrs[i]
         d.mlp = netv.struct()
         d.out_width, d.out_height = W, H
-        d.seed, d.jitter, d.mip_min, d.mip_max = 1234, 1.0, 0.0, 3.0
+        d.seed, d.jitter, d.mip_min, d.mip_max = 1234, jitter, mip_min, mip_max
         d.output = C.cast(out_ptr, abi.u16p)
         return d
 
@@ -398,7 +402,8 @@ def test_decode_from_codec_latents(lib, O):
     sync()
     got = gout.cpu().numpy().view(np.float16).astype(np.float32)
     assert rel_err(got, want.view(np.float16).astype(np.float32)) <= MLP_TOL
-    # The two-pass decode (blocks expanded to fp16 texels first) gives the same bits.
+    # The two-pass decode (blocks expanded to fp16 texels first, then sampled from per-block
+    # LDS boxes) gives the same bits.
     say("case: decode c4 two-pass")
     nbytes = lib.nt_decode_workspace_bytes(C.byref(gp))
     assert nbytes > 0
