@@ -206,14 +206,29 @@ __device__ __forceinline__ void to_fragments(const f16v (&acc)[NA], h8 (&y)[NQ])
 }
 
 // ReLU backward (mlp.h:240-252): dY_prev = fp16(acc) where the layer input x > 0, else 0.
+// x is a ReLU output (to_fragments: never negative, no -0), so x > 0 exactly when its bits
+// are nonzero: the mask min(bits, 1) multiplies the converted pair as 16-bit integers
+// (v_pk_min_u16, v_pk_mul_lo_u16 after one v_cvt_pk_f16_f32 per pair).
 template <int NQ, int NA>
 __device__ __forceinline__ void relu_backward(const f16v (&acc)[NA], const h8 (&x)[NQ], h8 (&dy)[NQ])
 {
+    // Written as instructions: the compiler turns the equivalent vector code into per-lane
+    // compares and lane masks.
+    const uint32_t ones = 0x00010001u;
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            dy[q][e] = x[q][e] > (_Float16)0.f ? (_Float16)acc[q >> 1][8 * (q & 1) + e] : (_Float16)0.f;
+        for (int e = 0; e < 8; e += 2) {
+            const f2 v = {acc[q >> 1][8 * (q & 1) + e], acc[q >> 1][8 * (q & 1) + e + 1]};
+            const uint32_t hv = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+            const h2 xv = {x[q][e], x[q][e + 1]};
+            uint32_t m, r;
+            asm("v_pk_min_u16 %0, %1, %2" : "=v"(m) : "v"(__builtin_bit_cast(uint32_t, xv)), "v"(ones));
+            asm("v_pk_mul_lo_u16 %0, %1, %2" : "=v"(r) : "v"(hv), "v"(m));
+            const h2 rh = __builtin_bit_cast(h2, r);
+            dy[q][e] = rh[0];
+            dy[q][e + 1] = rh[1];
+        }
 }
 
 // dX for one layer: acc[m] = W dY over the layer's output features (chained dY frags).
