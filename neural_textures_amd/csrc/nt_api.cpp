@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "nt_internal.hpp"
@@ -63,6 +64,26 @@ int hip_status(hipError_t e, const char *what)
 }
 
 constexpr int pad16(int x) { return (x + 15) & ~15; }
+
+// Compute units of the current device (256 on MI355X; also when no device is visible).
+int device_cu_count()
+{
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
 
 int mip_dim_h(int size, int mip)
 {
@@ -321,8 +342,18 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     const int tiles_y = (rows + kChunkH * NG - 1) / (kChunkH * NG);
     if ((int64_t)d.tiles_x * tiles_y > (1 << 30))
         return;
-    d.nwg = d.tiles_x * tiles_y;
-    d.xcd_per = d.nwg % 8 == 0 ? d.nwg / 8 : 0;
+    // One workgroup per CU (the kernel's registers and LDS allow no second one); each takes
+    // every nwg-th tile, so that fewer, longer-lived workgroups stage the weights and write
+    // MLP-gradient partials.
+    // NT_TRAIN_MAX_WORKGROUPS lowers the cap (tests use it to give workgroups several
+    // tiles at small sizes).
+    d.ntiles = d.tiles_x * tiles_y;
+    int cap = device_cu_count();
+    if (const char *env = std::getenv("NT_TRAIN_MAX_WORKGROUPS"))
+        if (std::atoi(env) > 0)
+            cap = std::min(cap, std::atoi(env));
+    d.nwg = std::min(d.ntiles, cap);
+    d.xcd_per = (d.ntiles % 8 == 0 && d.nwg % 8 == 0) ? d.ntiles / 8 : 0;
     int fp = 0, wcols = 0;
     for (int gi = 0; gi < G; ++gi) {
         const nt_grid &g = p->latents.grids[gi];

@@ -90,7 +90,7 @@ struct Train16Desc {
     int ntex;
     int image_w, image_h, off_x, off_y, region_w, num_samples;
     uint32_t step;
-    int tiles_x, nwg, xcd_per; // xcd_per > 0: workgroups of one XCD take consecutive tiles
+    int tiles_x, ntiles, nwg, xcd_per; // xcd_per > 0: workgroups of one XCD take consecutive tiles
     int fp_floats;
     int group_off, group_bytes, tile_bytes; // per 4-wave group: target tile, then the union
     int wcols;                              // halves per scatter-weight row (one row per sample)

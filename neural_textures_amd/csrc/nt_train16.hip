@@ -284,19 +284,6 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
             f4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    int b = blockIdx.x;
-    if (d.xcd_per > 0)
-        b = (b & 7) * d.xcd_per + (b >> 3); // the workgroups of one XCD share an L2: give them neighbouring tiles
-    const int tx0 = (b % d.tiles_x) * (kChunkW * 4), ty0 = (b / d.tiles_x) * (kChunkH * NG);
-    // Footprint box origin per grid: the lowest texel any sample of the workgroup can touch.
-    int flo_x[G], flo_y[G];
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        const Grid16 &q = d.grid[gi];
-        flo_x[gi] = (int)floorf((float)(d.off_x + tx0) * (float)q.w / (float)d.image_w - 0.5f) - 1;
-        flo_y[gi] = (int)floorf((float)(d.off_y + ty0) * (float)q.h / (float)d.image_h - 0.5f) - 1;
-    }
-
     f16v dwacc[LY::slots];
 #pragma unroll
     for (int j = 0; j < LY::slots; ++j)
@@ -305,8 +292,24 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 #pragma unroll
     for (int l = 0; l < L; ++l)
         dbacc[l] = 0.f;
-
     const int col = 32 * wave + c; // this lane's sample column in the group's transposes
+
+    // Tiles of the region, several per workgroup when there are more tiles than workgroups;
+    // the MLP gradient accumulates over all of them, the footprint box is flushed per tile.
+    for (int b0 = blockIdx.x; b0 < d.ntiles; b0 += gridDim.x) {
+    int b = b0;
+    if (d.xcd_per > 0)
+        b = (b & 7) * d.xcd_per + (b >> 3); // the workgroups of one XCD share an L2: give them neighbouring tiles
+    const int tx0 = (b % d.tiles_x) * (kChunkW * 4), ty0 = (b / d.tiles_x) * (kChunkH * NG);
+    // Footprint box origin per grid: the lowest texel any sample of the tile can touch.
+    int flo_x[G], flo_y[G];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        const Grid16 &q = d.grid[gi];
+        flo_x[gi] = (int)floorf((float)(d.off_x + tx0) * (float)q.w / (float)d.image_w - 0.5f) - 1;
+        flo_y[gi] = (int)floorf((float)(d.off_y + ty0) * (float)q.h / (float)d.image_h - 0.5f) - 1;
+    }
+
     for (int chunk = 0; chunk < 4; ++chunk) {
         const int cx0 = d.off_x + tx0 + chunk * kChunkW, cy0 = d.off_y + ty0 + kChunkH * gr;
         tile_fetch_async(d, tile, cx0, cy0, wave, lane);
@@ -502,16 +505,18 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     }
 
     __syncthreads();
-    // ---- flush the footprint box with global float atomics
+    // ---- flush the footprint box with global float atomics, clearing it for the next tile
+    // (the next tile's first box access follows at least one barrier)
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
         const Grid16 &q = d.grid[gi];
-        const float4 *box = (const float4 *)(fp + q.fp_off);
+        float4 *box = (float4 *)(fp + q.fp_off);
         const int n4 = q.fp_w * q.fp_h * 4;
         for (int i = tid; i < n4; i += kTrainThreads * NG) {
             const float4 val = box[i];
             if (val.x == 0.f && val.y == 0.f && val.z == 0.f && val.w == 0.f)
                 continue;
+            box[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             const int cell = i >> 2, part = i & 3;
             const int ly = (int)(((float)cell + 0.5f) * q.inv_fp_w), lx = cell - ly * q.fp_w;
             const int gx = wrap_near(flo_x[gi] + lx, q.w), gy = wrap_near(flo_y[gi] + ly, q.h);
@@ -526,6 +531,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                 global_add(dst + 3, val.w);
         }
     }
+    } // tiles
 
     // ---- the workgroup's MLP gradient partial (output rows of the last layer un-permuted):
     // group 1 hands its accumulators to group 0 through its own (now idle) LDS region.

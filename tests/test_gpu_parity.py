@@ -176,6 +176,22 @@ def test_train_step_gradients(lib, O, case):
             assert np.all(to_np(gg.block_grads) == 0)
 
 
+@pytest.mark.parametrize("shape", ["c2", "c4"])
+def test_train_step_several_tiles_per_workgroup(lib, O, shape, monkeypatch):
+    """Fewer workgroups than tiles: each workgroup runs several tiles, flushing its latent
+    box per tile and writing one MLP-gradient partial (the path large regions take)."""
+    say(f"case: train {shape} 3 workgroups for 4 tiles")
+    monkeypatch.setenv("NT_TRAIN_MAX_WORKGROUPS", "3")
+    st, gs = run_train_pair(lib, O, shape, 128, (128, 32 if shape == "c2" else 16), (5, 9),
+                            abi.NT_UNCONSTRAINED)
+    for l in range(st.net.num_layers):
+        assert rel_err(to_np(gs.net.weight_grads[l]), st.net.weight_grads[l]) <= MLP_TOL, f"dW{l}"
+        assert rel_err(to_np(gs.net.bias_grads[l]), st.net.bias_grads[l]) <= MLP_TOL, f"db{l}"
+    for gi, (g, gg) in enumerate(zip(st.grids, gs.grids)):
+        assert rel_err(to_np(gg.grads), g.grads) <= MLP_TOL, f"latent grad {gi}"
+        assert np.all(to_np(gg.grads)[g.grads == 0] == 0)
+
+
 def test_train_step_accumulates(lib, O):
     """Two passes without an optimizer step add up (the zero-gradient contract)."""
     say("case: train accumulate")
