@@ -25,12 +25,17 @@ __global__ __launch_bounds__(256) void net_adam_kernel(NetAdamDesc d)
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= d.wstart[d.num_layers])
         return;
+    // Layers start at multiples of 256 items: the layer is uniform per workgroup and its
+    // pointers come from scalar loads.
     int l = 0;
     for (int k = 1; k < d.num_layers; ++k)
-        if (i >= d.wstart[k])
+        if ((int)(blockIdx.x * 256) >= d.wstart[k])
             l = k;
+    l = __builtin_amdgcn_readfirstlane(l);
     const int local = i - d.wstart[l];
     const int nw = d.rows[l] * d.cols[l];
+    if (local >= nw + d.nbias[l])
+        return; // padding to the next layer's start
     if (local < nw) {
         // OptimizePaddedParameterMatrix (train.cu:590-623): active rows x cols only.
         const int row = local % d.rows[l], col = local / d.rows[l];
@@ -61,6 +66,18 @@ __global__ __launch_bounds__(256) void net_adam_kernel(NetAdamDesc d)
     }
 }
 
+// Segment (grid) of the workgroup's current 256 work items: segments start at multiples of
+// 256 items, so it is uniform and the segment's pointers come from scalar loads.
+__device__ __forceinline__ int adam_segment(const LatentAdamDesc &d, int64_t block_first)
+{
+    int s = 0;
+#pragma unroll
+    for (int k = 1; k < NT_MAX_GRIDS; ++k)
+        if (k < d.nseg && block_first >= d.start[k])
+            s = k;
+    return __builtin_amdgcn_readfirstlane(s);
+}
+
 // Unconstrained latents: work item = 4 consecutive floats of one grid's flattened mip chain
 // (OptimizeUnconstrainedFeaturePass, train.cu:764-803).
 __global__ __launch_bounds__(256) void latent_adam_kernel(LatentAdamDesc d)
@@ -68,11 +85,7 @@ __global__ __launch_bounds__(256) void latent_adam_kernel(LatentAdamDesc d)
     const int64_t total = d.start[d.nseg];
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * 256) {
-        int s = 0;
-#pragma unroll
-        for (int k = 1; k < NT_MAX_GRIDS; ++k)
-            if (k < d.nseg && i >= d.start[k])
-                s = k;
+        const int s = adam_segment(d, i - threadIdx.x);
         const int64_t f0 = (i - d.start[s]) * 4;
         const int64_t rem = d.n[s] - f0;
         float *g = d.g[s] + f0;
@@ -118,12 +131,10 @@ __global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
     const int rec = d.rec;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * 256) {
-        int s = 0;
-#pragma unroll
-        for (int k = 1; k < NT_MAX_GRIDS; ++k)
-            if (k < d.nseg && i >= d.start[k])
-                s = k;
+        const int s = adam_segment(d, i - threadIdx.x);
         const int64_t b = i - d.start[s];
+        if (b >= d.n[s])
+            continue; // padding to the next segment's start
         float *w = d.w[s] + b * (rec + 2);
         float *g = d.g[s] + b * rec;
         float *m1 = d.m1[s] + b * rec;

@@ -229,7 +229,7 @@ struct NetAdamDesc {
     AdamDesc a;
     int num_layers;
     int rows[NT_MAX_LAYERS], cols[NT_MAX_LAYERS], pin[NT_MAX_LAYERS], nbias[NT_MAX_LAYERS];
-    int wstart[NT_MAX_LAYERS + 1]; // prefix over layers of rows*cols + nbias
+    int wstart[NT_MAX_LAYERS + 1]; // prefix over layers of rows*cols + nbias, each padded to 256
     uint16_t *w[NT_MAX_LAYERS];
     float *g[NT_MAX_LAYERS], *m1[NT_MAX_LAYERS], *m2[NT_MAX_LAYERS];
     uint16_t *b[NT_MAX_LAYERS];
@@ -240,7 +240,7 @@ struct NetAdamDesc {
 struct LatentAdamDesc {
     AdamDesc a;
     int nseg;
-    int64_t start[NT_MAX_GRIDS + 1]; // prefix of work items
+    int64_t start[NT_MAX_GRIDS + 1]; // prefix of work items, each segment padded to 256
     float *w[NT_MAX_GRIDS], *g[NT_MAX_GRIDS], *m1[NT_MAX_GRIDS], *m2[NT_MAX_GRIDS];
     int64_t n[NT_MAX_GRIDS]; // floats (unconstrained) or blocks (block records)
     int rec;                 // block record floats (4C+16); 0 = unconstrained

@@ -889,34 +889,39 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 
 // Two-stage deterministic reduction of the per-workgroup partials into the network
 // gradients (which the contract says are accumulated into, train.cu:1028-1048).
-// partial[rows][P] -> the MLP gradients, in one pass and a fixed order: a workgroup owns 64
-// parameters; wave w sums rows [w R/4, (w+1) R/4) in row order over four interleaved
-// accumulators, and the four wave sums are added in wave order. The same bits on every run.
+// partial[rows][P] -> the MLP gradients, in one pass and a fixed order: a workgroup owns 16
+// parameters and splits the rows into 16 contiguous groups, one per 16-lane slice; each
+// lane sums its group's rows in row order (all loads issued before the adds), then lane
+// group 0 adds the 16 group sums in group order. The same bits on every run.
+constexpr int kReduceCols = 16, kReduceGroups = 16, kReduceUnroll = 16;
 __global__ __launch_bounds__(256) void reduce_rows(ReduceDesc d)
 {
-    __shared__ float part[4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int p = blockIdx.x * 64 + lane;
-    const int per = (d.rows + 3) / 4;
-    const int r0 = wave * per, r1 = min(r0 + per, d.rows);
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    __shared__ float part[kReduceGroups][kReduceCols];
+    const int col = threadIdx.x % kReduceCols, grp = threadIdx.x / kReduceCols;
+    const int p = blockIdx.x * kReduceCols + col;
+    const int per = (d.rows + kReduceGroups - 1) / kReduceGroups;
+    const int r0 = grp * per, r1 = min(r0 + per, d.rows);
+    float sum = 0.f;
     if (p < d.P) {
-        const float *col = d.partial + p;
-        int r = r0;
-        for (; r + 4 <= r1; r += 4) {
-            s0 += col[(int64_t)r * d.P];
-            s1 += col[(int64_t)(r + 1) * d.P];
-            s2 += col[(int64_t)(r + 2) * d.P];
-            s3 += col[(int64_t)(r + 3) * d.P];
+        const float *c = d.partial + p;
+        for (int r = r0; r < r1; r += kReduceUnroll) {
+            float v[kReduceUnroll];
+#pragma unroll
+            for (int k = 0; k < kReduceUnroll; ++k)
+                v[k] = r + k < r1 ? c[(int64_t)(r + k) * d.P] : 0.f;
+#pragma unroll
+            for (int k = 0; k < kReduceUnroll; ++k)
+                sum += v[k];
         }
-        for (; r < r1; ++r)
-            s0 += col[(int64_t)r * d.P];
     }
-    part[wave][lane] = (s0 + s1) + (s2 + s3);
+    part[grp][col] = sum;
     __syncthreads();
-    if (wave != 0 || p >= d.P)
+    if (grp != 0 || p >= d.P)
         return;
-    const float s = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kReduceGroups; ++k)
+        s += part[k][col];
     int l = 0;
     for (int k = 1; k < d.num_layers; ++k)
         if (p >= d.off[k])
@@ -953,7 +958,7 @@ static hipError_t launch_prep(const PrepDesc &d, hipStream_t s)
 
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s)
 {
-    hipLaunchKernelGGL(reduce_rows, dim3((d.P + 63) / 64), dim3(256), 0, s, d);
+    hipLaunchKernelGGL(reduce_rows, dim3((d.P + kReduceCols - 1) / kReduceCols), dim3(256), 0, s, d);
     return hipGetLastError();
 }
 
