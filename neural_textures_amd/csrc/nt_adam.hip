@@ -66,8 +66,8 @@ __global__ __launch_bounds__(256) void net_adam_kernel(NetAdamDesc d)
     }
 }
 
-// Segment (grid) of the workgroup's current 256 work items: segments start at multiples of
-// 256 items, so it is uniform and the segment's pointers come from scalar loads.
+// Segment (grid) of the workgroup's current work items: segments start at multiples of
+// kAdamSpan items, so it is uniform and the segment's pointers come from scalar loads.
 __device__ __forceinline__ int adam_segment(const LatentAdamDesc &d, int64_t block_first)
 {
     int s = 0;
@@ -78,48 +78,63 @@ __device__ __forceinline__ int adam_segment(const LatentAdamDesc &d, int64_t blo
     return __builtin_amdgcn_readfirstlane(s);
 }
 
+// One work item: 4 consecutive floats with their gradient already loaded.
+__device__ __forceinline__ void latent_adam_item(const LatentAdamDesc &d, int s, int64_t f0, float4 gv)
+{
+    const int64_t rem = d.n[s] - f0;
+    float *g = d.g[s] + f0;
+    if (rem >= 4) {
+        if (gv.x == 0.f && gv.y == 0.f && gv.z == 0.f && gv.w == 0.f)
+            return;
+        float4 wv = *(const float4 *)(d.w[s] + f0);
+        float4 m1 = *(const float4 *)(d.m1[s] + f0);
+        float4 m2 = *(const float4 *)(d.m2[s] + f0);
+        if (gv.x != 0.f)
+            wv.x = adam_update(m1.x, m2.x, gv.x, d.a, wv.x);
+        if (gv.y != 0.f)
+            wv.y = adam_update(m1.y, m2.y, gv.y, d.a, wv.y);
+        if (gv.z != 0.f)
+            wv.z = adam_update(m1.z, m2.z, gv.z, d.a, wv.z);
+        if (gv.w != 0.f)
+            wv.w = adam_update(m1.w, m2.w, gv.w, d.a, wv.w);
+        *(float4 *)(d.w[s] + f0) = wv;
+        *(float4 *)(d.m1[s] + f0) = m1;
+        *(float4 *)(d.m2[s] + f0) = m2;
+        *(float4 *)g = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+        for (int k = 0; k < rem; ++k) {
+            const float gs = g[k];
+            if (gs == 0.f)
+                continue;
+            float m1 = d.m1[s][f0 + k], m2 = d.m2[s][f0 + k];
+            d.w[s][f0 + k] = adam_update(m1, m2, gs, d.a, d.w[s][f0 + k]);
+            d.m1[s][f0 + k] = m1;
+            d.m2[s][f0 + k] = m2;
+            g[k] = 0.f;
+        }
+    }
+}
+
 // Unconstrained latents: work item = 4 consecutive floats of one grid's flattened mip chain
-// (OptimizeUnconstrainedFeaturePass, train.cu:764-803).
+// (OptimizeUnconstrainedFeaturePass, train.cu:764-803). A workgroup takes kAdamSpan items
+// at a time, thread t the items t + 256k: all four gradient loads are issued before any is
+// tested (almost all gradients are zero; the scan is what costs).
 __global__ __launch_bounds__(256) void latent_adam_kernel(LatentAdamDesc d)
 {
+    constexpr int K = kAdamSpan / 256;
     const int64_t total = d.start[d.nseg];
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * 256) {
-        const int s = adam_segment(d, i - threadIdx.x);
-        const int64_t f0 = (i - d.start[s]) * 4;
-        const int64_t rem = d.n[s] - f0;
-        float *g = d.g[s] + f0;
-        if (rem >= 4) {
-            float4 gv = *(const float4 *)g;
-            if (gv.x == 0.f && gv.y == 0.f && gv.z == 0.f && gv.w == 0.f)
-                continue;
-            float4 wv = *(const float4 *)(d.w[s] + f0);
-            float4 m1 = *(const float4 *)(d.m1[s] + f0);
-            float4 m2 = *(const float4 *)(d.m2[s] + f0);
-            if (gv.x != 0.f)
-                wv.x = adam_update(m1.x, m2.x, gv.x, d.a, wv.x);
-            if (gv.y != 0.f)
-                wv.y = adam_update(m1.y, m2.y, gv.y, d.a, wv.y);
-            if (gv.z != 0.f)
-                wv.z = adam_update(m1.z, m2.z, gv.z, d.a, wv.z);
-            if (gv.w != 0.f)
-                wv.w = adam_update(m1.w, m2.w, gv.w, d.a, wv.w);
-            *(float4 *)(d.w[s] + f0) = wv;
-            *(float4 *)(d.m1[s] + f0) = m1;
-            *(float4 *)(d.m2[s] + f0) = m2;
-            *(float4 *)g = make_float4(0.f, 0.f, 0.f, 0.f);
-        } else {
-            for (int k = 0; k < rem; ++k) {
-                const float gs = g[k];
-                if (gs == 0.f)
-                    continue;
-                float m1 = d.m1[s][f0 + k], m2 = d.m2[s][f0 + k];
-                d.w[s][f0 + k] = adam_update(m1, m2, gs, d.a, d.w[s][f0 + k]);
-                d.m1[s][f0 + k] = m1;
-                d.m2[s][f0 + k] = m2;
-                g[k] = 0.f;
-            }
+    for (int64_t base = (int64_t)blockIdx.x * kAdamSpan; base < total; base += (int64_t)gridDim.x * kAdamSpan) {
+        const int s = adam_segment(d, base);
+        const int64_t f = (base - d.start[s] + threadIdx.x) * 4;
+        float4 gv[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int64_t fk = f + 1024 * k;
+            gv[k] = fk + 4 <= d.n[s] ? *(const float4 *)(d.g[s] + fk) : make_float4(1.f, 1.f, 1.f, 1.f);
         }
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            latent_adam_item(d, s, f + 1024 * k, gv[k]);
     }
 }
 
@@ -166,7 +181,7 @@ hipError_t launch_latent_adam(const LatentAdamDesc &d, hipStream_t s)
     const int64_t n = d.start[d.nseg];
     if (n <= 0)
         return hipSuccess;
-    int64_t blocks = (n + 255) / 256;
+    int64_t blocks = d.rec > 0 ? (n + 255) / 256 : (n + kAdamSpan - 1) / kAdamSpan;
     if (blocks > 8192)
         blocks = 8192;
     if (d.rec > 0)

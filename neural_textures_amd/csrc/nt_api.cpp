@@ -821,7 +821,7 @@ int nt_optimize_latents(const nt_params *p, nt_kernel_type type, void *stream)
             d.m1[gi] = g.moment1 + base;
             d.m2[gi] = g.moment2 + base;
             d.n[gi] = texels * C;
-            start += ((d.n[gi] + 3) / 4 + 255) / 256 * 256; // segments start at whole workgroups
+            start += ((d.n[gi] + 3) / 4 + kAdamSpan - 1) / kAdamSpan * kAdamSpan; // whole workgroup spans
         } else {
             int64_t nb = 0;
             for (int m = 0; m < g.num_mips; ++m) {
@@ -837,7 +837,7 @@ int nt_optimize_latents(const nt_params *p, nt_kernel_type type, void *stream)
             d.m1[gi] = g.block_moment1 + g.block_offset[0] * (4 * C + 16);
             d.m2[gi] = g.block_moment2 + g.block_offset[0] * (4 * C + 16);
             d.n[gi] = nb;
-            start += (nb + 255) / 256 * 256;
+            start += (nb + kAdamSpan - 1) / kAdamSpan * kAdamSpan;
         }
     }
     d.start[lat.num_grids] = start;

@@ -236,11 +236,13 @@ struct NetAdamDesc {
     float *bg[NT_MAX_LAYERS], *bm1[NT_MAX_LAYERS], *bm2[NT_MAX_LAYERS];
 };
 
-// Lazy Adam over flat fp32 segments (latent texels or BC6 block records).
+// Lazy Adam over flat fp32 segments (latent texels or BC6 block records). Segments start at
+// multiples of kAdamSpan work items.
+constexpr int kAdamSpan = 1024;
 struct LatentAdamDesc {
     AdamDesc a;
     int nseg;
-    int64_t start[NT_MAX_GRIDS + 1]; // prefix of work items, each segment padded to 256
+    int64_t start[NT_MAX_GRIDS + 1]; // prefix of work items, each segment padded to kAdamSpan
     float *w[NT_MAX_GRIDS], *g[NT_MAX_GRIDS], *m1[NT_MAX_GRIDS], *m2[NT_MAX_GRIDS];
     int64_t n[NT_MAX_GRIDS]; // floats (unconstrained) or blocks (block records)
     int rec;                 // block record floats (4C+16); 0 = unconstrained
