@@ -171,11 +171,18 @@ __device__ __forceinline__ void layer_forward(const h8 *frags, const float *bias
                                               f16v (&acc)[NA], int lane)
 {
     const int g = lane >> 5;
+    // Rows 32a + 8j + 4g .. +3 of the bias are one 16-byte LDS read (bias is 16-byte aligned).
+    const float4 *b4 = (const float4 *)(bias + 4 * g);
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-            acc[a][e] = bias[32 * a + 8 * (e >> 2) + 4 * g + (e & 3)];
+        for (int j = 0; j < 4; ++j) {
+            const float4 v = b4[8 * a + 2 * j];
+            acc[a][4 * j] = v.x;
+            acc[a][4 * j + 1] = v.y;
+            acc[a][4 * j + 2] = v.z;
+            acc[a][4 * j + 3] = v.w;
+        }
 #pragma unroll
         for (int q = 0; q < KQ; ++q)
             acc[a] = mfma32(frags[(a * KQ + q) * kWave + lane], x[q], acc[a]);
