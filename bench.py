@@ -104,7 +104,7 @@ def build_config2(device, seed=1337):
     return build_config(device, 2, seed)
 
 
-def bench_train(lib, nt, args, ev, cfg=2, steps=None, warmup=None):
+def bench_train(lib, nt, args, ev, cfg=2, steps=None, warmup=None, sample_mode=0):
     import torch
 
     from neural_textures_amd import abi
@@ -113,6 +113,7 @@ def bench_train(lib, nt, args, ev, cfg=2, steps=None, warmup=None):
     steps = args.steps if steps is None else steps
     warmup = args.warmup if warmup is None else warmup
     st = build_config(device, cfg)
+    st.sample_mode = sample_mode
     image, region = st.image_width, st.region_width
     p = st.params()
     ws_bytes = lib.nt_train_workspace_bytes(C.byref(p), abi.NT_UNCONSTRAINED)
@@ -388,6 +389,18 @@ def main():
                          "achieved": ach4, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                          "frac": ach4 / PEAK_FP16_TFLOPS, "launch_ms_mean": k4}}
         del st4
+        log("bench: config 2 train steps, uniform-random texels")
+        str_, msr, kr, _ = bench_train(lib, nt, args, ev, cfg=2, steps=20, warmup=5, sample_mode=1)
+        achr = FLOP_PER_TRAIN_SAMPLE_C2 * 262144 / (kr / 1e3) / 1e12
+        result["train_config2_random_texels"] = {
+            "value": 262144 / (msr / 1e3), "unit": "texels/s", "ms_per_step": msr, "steps": 20,
+            "workload": "config 2 with NT_SAMPLES_RANDOM: 262,144 samples at uniformly random "
+                        "texels of the whole 2048^2 image (no region locality: gathers, target "
+                        "taps and latent-gradient atomics all go to L2/HBM)",
+            "roofline": {"kernel": "train_kernel<Shape<32,64,2>,16,UNCONSTRAINED>", "bound": "mfma",
+                         "achieved": achr, "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": achr / PEAK_FP16_TFLOPS, "launch_ms_mean": kr}}
+        del str_
         log("bench: config 5 decode")
         dms, kms, npx, wsb = bench_decode(lib, nt, ev)
         dach = FLOP_PER_DECODE_PIXEL * npx / (kms / 1e3) / 1e12
@@ -396,7 +409,7 @@ def main():
                                         "(4 grids 16ch 1024..128, mips 9..6), jitter + z~U[0,3]; "
                                         "two passes (block expand to fp16 texels + sample/MLP)",
                             "workspace_bytes": wsb,
-                            "roofline": {"kernel": "forward_kernel<Shape<64,64,3>,16,Decode16>",
+                            "roofline": {"kernel": "decode_box_kernel<Shape<64,64,3>>",
                                          "bound": "mfma", "achieved": dach, "peak": PEAK_FP16_TFLOPS,
                                          "unit": "TFLOP/s", "frac": dach / PEAK_FP16_TFLOPS,
                                          "launch_ms_mean": kms}}

@@ -75,6 +75,22 @@ typedef enum nt_filter {
     NT_FILTER_CATMULL_ROM = 1 /* 16-tap Catmull-Rom on mip 0 (forward only, nt_forward) */
 } nt_filter;
 
+/*
+ * Where the samples of a train step sit. NT_SAMPLES_REGION is the reference's
+ * (train.cu:827-844): sample i at texel (texel_offset_x + i % region_width,
+ * texel_offset_y + i / region_width), jittered by U[-0.5, 0.5) per axis. NT_SAMPLES_RANDOM
+ * (no reference counterpart): sample i at a uniformly random texel of the whole image,
+ * x = min(floor(U(h1) * image_width), image_width - 1), y likewise from U(h2), then the
+ * same jitter; h1 = fmix32(seed), h2 = fmix32(h1) with fmix32 the MurmurHash3 finalizer and
+ * seed the sample's RNG seed (train.cu:833), U(h) = (h & 0xFFFFFF) * 2^-24. (The
+ * reference's xorshift draws of consecutive seeds are too correlated to place texels.)
+ * Region fields are unused.
+ */
+typedef enum nt_sample_mode {
+    NT_SAMPLES_REGION = 0,
+    NT_SAMPLES_RANDOM = 1
+} nt_sample_mode;
+
 /* Mirrors AdamConstants (train.h:29-35). */
 typedef struct nt_adam {
     float beta1;
@@ -179,6 +195,7 @@ typedef struct nt_params {
     int region_width;   /* samples per region row; 0 means NT_DEFAULT_REGION */
     int num_samples;    /* batch size; sample i sits at (i % region_width, i / region_width) */
     int step;           /* Adam step; bias correction uses max(step, 1) (train.cu:528) */
+    int sample_mode;    /* NT_SAMPLES_REGION (the reference) or NT_SAMPLES_RANDOM */
 
     float *inference_output;   /* nt_inference: [pixel][sizes[num_layers]] fp32 */
     float *inference_mse_accum; /* nt_inference: SSE accumulator (one float) */

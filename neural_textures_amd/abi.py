@@ -35,6 +35,10 @@ NT_UNCONSTRAINED = 0
 NT_BLOCK_FEATURES = 1
 NT_FINALIZE = 2
 
+# nt_sample_mode
+NT_SAMPLES_REGION = 0
+NT_SAMPLES_RANDOM = 1
+
 # nt_filter
 NT_FILTER_BILINEAR = 0
 NT_FILTER_CATMULL_ROM = 1
@@ -98,6 +102,7 @@ class nt_params(C.Structure):
         ("image_width", C.c_int), ("image_height", C.c_int),
         ("texel_offset_x", C.c_int), ("texel_offset_y", C.c_int),
         ("region_width", C.c_int), ("num_samples", C.c_int), ("step", C.c_int),
+        ("sample_mode", C.c_int),
         ("inference_output", f32p), ("inference_mse_accum", f32p),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
     ]

@@ -296,7 +296,8 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->use16 = 0;
     const int NG = train16_groups(plan->shape);
     const int C = p->latents.channels, G = p->latents.num_grids;
-    if (type != NT_UNCONSTRAINED || C != 16 || NG == 0 || p->num_textures < 1 || p->num_textures > 4)
+    if (type != NT_UNCONSTRAINED || C != 16 || NG == 0 || p->num_textures < 1 || p->num_textures > 4 ||
+        p->sample_mode != NT_SAMPLES_REGION)
         return;
     Train16Desc &d = plan->t16;
     d = Train16Desc{};
@@ -433,6 +434,8 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         return fail(NT_ERR_INVALID_ARGUMENT, "image size %dx%d", p->image_width, p->image_height);
     if (p->num_samples < 1)
         return fail(NT_ERR_INVALID_ARGUMENT, "num_samples %d", p->num_samples);
+    if (p->sample_mode != NT_SAMPLES_REGION && p->sample_mode != NT_SAMPLES_RANDOM)
+        return fail(NT_ERR_INVALID_ARGUMENT, "sample_mode %d", p->sample_mode);
     const int rw = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
     const int rows = (int)(((int64_t)p->num_samples + rw - 1) / rw);
     plan->shape = shape;
@@ -491,7 +494,12 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             un = scatter;
         return un;
     };
-    plan->fp_floats = type == NT_UNCONSTRAINED ? fp : 0;
+    // Random texels have no spatial locality within a workgroup: no footprint box, value
+    // box or target tile; gathers, taps and scatter atomics go to global memory.
+    const bool random = p->sample_mode == NT_SAMPLES_RANDOM;
+    if (random)
+        plan->tile_ok = 0;
+    plan->fp_floats = type == NT_UNCONSTRAINED && !random ? fp : 0;
     if (plan->fp_floats && head + fp_bytes(plan->fp_floats) + union_bytes(false, false) > kMaxLds)
         plan->fp_floats = 0; // box does not fit: scatter straight to global memory
     // With 16 channels the latent values under the box are staged in LDS too, so the
@@ -687,6 +695,7 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     d.vbox_floats = plan.vbox_floats;
     d.vbox_off = plan.vbox_off;
     d.tile_ok = plan.tile_ok;
+    d.random_texels = p->sample_mode == NT_SAMPLES_RANDOM;
     d.scatter_mfma = plan.scatter_mfma;
     d.w_rows = plan.w_rows;
     d.union_off = plan.union_off;

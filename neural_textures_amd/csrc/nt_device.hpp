@@ -135,6 +135,17 @@ __device__ __forceinline__ uint32_t mix_seed(uint32_t index, uint32_t step)
     return s ? s : 1u;
 }
 
+// MurmurHash3's 32-bit finalizer (public domain): places NT_SAMPLES_RANDOM samples.
+__device__ __forceinline__ uint32_t fmix32(uint32_t h)
+{
+    h ^= h >> 16;
+    h *= 0x85EBCA6Bu;
+    h ^= h >> 13;
+    h *= 0xC2B2AE35u;
+    h ^= h >> 16;
+    return h;
+}
+
 __device__ __forceinline__ float clampf(float x, float lo, float hi)
 {
     return x < lo ? lo : (x > hi ? hi : x);

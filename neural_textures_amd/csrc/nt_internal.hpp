@@ -60,6 +60,7 @@ struct TrainDesc {
     int vbox_floats; // LDS copy of the latent values under the footprint box (C = 16; 0: gather from HBM)
     int vbox_off;    // its byte offset in LDS
     int tile_ok;    // the chunk's target taps are staged in LDS (textures match the image size)
+    int random_texels; // NT_SAMPLES_RANDOM: sample positions anywhere in the image
     int scatter_mfma; // latent scatter as an MFMA reduction over the chunk (else LDS atomics)
     int w_rows;     // rows of each bilinear-weight matrix (all grids, 16-row tiles)
     int union_off;  // byte offset of the LDS region shared by tile / transposes (/ scatter)

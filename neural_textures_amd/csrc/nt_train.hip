@@ -686,12 +686,19 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
         const uint32_t sidx = (uint32_t)sy * (uint32_t)d.region_w + (uint32_t)sx;
         const bool valid = sx < d.region_w && sidx < (uint32_t)d.num_samples;
         uint32_t st = mix_seed(sidx, d.step);
+        uint32_t tx = (uint32_t)(d.off_x + sx), ty = (uint32_t)(d.off_y + sy);
+        if (d.random_texels) {
+            // A uniformly random texel of the image, then the jitter (NT_SAMPLES_RANDOM).
+            const uint32_t h1 = fmix32(st), h2 = fmix32(h1);
+            const uint32_t rx = (uint32_t)((float)(h1 & 0x00FFFFFFu) * (1.0f / 16777216.0f) * (float)d.image_w);
+            const uint32_t ry = (uint32_t)((float)(h2 & 0x00FFFFFFu) * (1.0f / 16777216.0f) * (float)d.image_h);
+            tx = rx < (uint32_t)d.image_w ? rx : (uint32_t)d.image_w - 1;
+            ty = ry < (uint32_t)d.image_h ? ry : (uint32_t)d.image_h - 1;
+        }
         const float jx = uniform01(st) - 0.5f;
         const float jy = uniform01(st) - 0.5f;
-        const float px = clampf((float)(uint32_t)(d.off_x + sx) + 0.5f + jx, 0.5f,
-                                (float)d.image_w - 0.5f);
-        const float py = clampf((float)(uint32_t)(d.off_y + sy) + 0.5f + jy, 0.5f,
-                                (float)d.image_h - 0.5f);
+        const float px = clampf((float)tx + 0.5f + jx, 0.5f, (float)d.image_w - 0.5f);
+        const float py = clampf((float)ty + 0.5f + jy, 0.5f, (float)d.image_h - 0.5f);
         const float u = px / (float)d.image_w;
         const float v = py / (float)d.image_h;
 

@@ -229,6 +229,7 @@ class TrainState:
     workspace: object = None
     inference_output: object = None
     inference_mse_accum: object = None
+    sample_mode: int = abi.NT_SAMPLES_REGION
 
     @property
     def channels(self) -> int:
@@ -249,6 +250,7 @@ class TrainState:
         p.image_width, p.image_height = self.image_width, self.image_height
         p.texel_offset_x, p.texel_offset_y = self.texel_offset_x, self.texel_offset_y
         p.region_width, p.num_samples, p.step = self.region_width, self.num_samples, self.step
+        p.sample_mode = self.sample_mode
         p.inference_output = pointer(self.inference_output)
         p.inference_mse_accum = pointer(self.inference_mse_accum)
         if self.workspace is not None:
@@ -266,7 +268,7 @@ class TrainState:
             self.texel_offset_x, self.texel_offset_y, self.step, self.network_adam,
             self.feature_adam, None,
             _copy(self.inference_output, to_torch, device),
-            _copy(self.inference_mse_accum, to_torch, device))
+            _copy(self.inference_mse_accum, to_torch, device), self.sample_mode)
 
     def to_torch(self, device="cuda") -> "TrainState":
         return self.converted(True, device)

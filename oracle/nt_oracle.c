@@ -127,12 +127,31 @@ static int mip_dim(int size, int mip)
     return d > 0 ? d : 1;
 }
 
+uint32_t ntref_fmix32(uint32_t h)
+{
+    /* MurmurHash3's 32-bit finalizer (public domain, Austin Appleby). */
+    h ^= h >> 16;
+    h *= 0x85EBCA6Bu;
+    h ^= h >> 13;
+    h *= 0xC2B2AE35u;
+    h ^= h >> 16;
+    return h;
+}
+
 void ntref_sample_uvz(const nt_params *p, uint32_t i, float uvz[3])
 {
     const uint32_t rw = p->region_width > 0 ? (uint32_t)p->region_width : NT_DEFAULT_REGION;
-    const uint32_t sx = (uint32_t)p->texel_offset_x + i % rw;
-    const uint32_t sy = (uint32_t)p->texel_offset_y + i / rw;
+    uint32_t sx = (uint32_t)p->texel_offset_x + i % rw;
+    uint32_t sy = (uint32_t)p->texel_offset_y + i / rw;
     uint32_t st = ntref_sample_seed(i, p->step);
+    if (p->sample_mode == NT_SAMPLES_RANDOM) {
+        /* A uniformly random texel of the image (nt.h nt_sample_mode), then the jitter. */
+        const uint32_t h1 = ntref_fmix32(st), h2 = ntref_fmix32(h1);
+        const uint32_t x = (uint32_t)((float)(h1 & 0x00FFFFFFu) * (1.0f / 16777216.0f) * (float)p->image_width);
+        const uint32_t y = (uint32_t)((float)(h2 & 0x00FFFFFFu) * (1.0f / 16777216.0f) * (float)p->image_height);
+        sx = x < (uint32_t)p->image_width ? x : (uint32_t)p->image_width - 1;
+        sy = y < (uint32_t)p->image_height ? y : (uint32_t)p->image_height - 1;
+    }
     const float jx = ntref_uniform(&st) - 0.5f;
     const float jy = ntref_uniform(&st) - 0.5f;
     const float px = clampf((float)sx + 0.5f + jx, 0.5f, (float)p->image_width - 0.5f);

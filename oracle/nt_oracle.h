@@ -44,7 +44,10 @@ uint32_t ntref_xorshift32(uint32_t *state);
 float ntref_uniform(uint32_t *state);
 uint32_t ntref_sample_seed(uint32_t sample_index, int step);
 
-/* Sample position of sample i (train.cu:827-844): writes (u, v, 0). */
+/* MurmurHash3's 32-bit finalizer (texel placement of NT_SAMPLES_RANDOM). */
+uint32_t ntref_fmix32(uint32_t h);
+/* Sample position of sample i (train.cu:827-844; NT_SAMPLES_RANDOM as nt.h defines it):
+ * writes (u, v, 0). */
 void ntref_sample_uvz(const nt_params *p, uint32_t sample_index, float uvz[3]);
 
 /* Latent sampling: bilinear/trilinear with fp16 accumulation (train.cu:263-314). */

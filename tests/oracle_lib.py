@@ -18,6 +18,7 @@ SIGNATURES = {
     "ntref_xorshift32": (C.c_uint32, [P(C.c_uint32)]),
     "ntref_uniform": (C.c_float, [P(C.c_uint32)]),
     "ntref_sample_seed": (C.c_uint32, [C.c_uint32, C.c_int]),
+    "ntref_fmix32": (C.c_uint32, [C.c_uint32]),
     "ntref_sample_uvz": (None, [P(abi.nt_params), C.c_uint32, P(C.c_float)]),
     "ntref_sample_latents_bilinear": (None, [P(abi.nt_latents), P(C.c_float), P(C.c_uint16)]),
     "ntref_sample_latents_catmull_rom": (None, [P(abi.nt_latents), P(C.c_float), P(C.c_uint16)]),

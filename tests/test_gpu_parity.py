@@ -192,6 +192,25 @@ def test_train_step_several_tiles_per_workgroup(lib, O, shape, monkeypatch):
         assert np.all(to_np(gg.grads)[g.grads == 0] == 0)
 
 
+@pytest.mark.parametrize("shape", ["ref", "c2", "c4"])
+def test_train_step_random_texels(lib, O, shape):
+    """NT_SAMPLES_RANDOM: samples anywhere in the image (no footprint box or target tile);
+    gradients match the oracle's at the MLP tolerance."""
+    say(f"case: train {shape} random texels")
+    st = make_state(shape, image=128, region=(64, 32), seed=17)
+    st.sample_mode = abi.NT_SAMPLES_RANDOM
+    gs = gpu_workspace(lib, st.to_torch(), abi.NT_UNCONSTRAINED)
+    assert O.ntref_train_step(C.byref(st.params()), abi.NT_UNCONSTRAINED, 1) == 0
+    nt.check(lib.nt_train_step(C.byref(gs.params()), abi.NT_UNCONSTRAINED, None))
+    sync()
+    for l in range(st.net.num_layers):
+        assert rel_err(to_np(gs.net.weight_grads[l]), st.net.weight_grads[l]) <= MLP_TOL, f"dW{l}"
+        assert rel_err(to_np(gs.net.bias_grads[l]), st.net.bias_grads[l]) <= MLP_TOL, f"db{l}"
+    for gi, (g, gg) in enumerate(zip(st.grids, gs.grids)):
+        assert rel_err(to_np(gg.grads), g.grads) <= MLP_TOL, f"latent grad {gi}"
+        assert np.all(to_np(gg.grads)[g.grads == 0] == 0)
+
+
 def test_train_step_accumulates(lib, O):
     """Two passes without an optimizer step add up (the zero-gradient contract)."""
     say("case: train accumulate")

@@ -79,6 +79,55 @@ def test_sample_position_region_and_clamp():
         assert uvz[2] == 0.0
 
 
+def test_fmix32_known_answers():
+    """MurmurHash3 fmix32 (the published finalizer): fixed point 0, and values computed by
+    its three xor-shift / multiply rounds done here in Python integers."""
+    def fmix(h):
+        h ^= h >> 16
+        h = (h * 0x85EBCA6B) & 0xFFFFFFFF
+        h ^= h >> 13
+        h = (h * 0xC2B2AE35) & 0xFFFFFFFF
+        return h ^ (h >> 16)
+    assert O.ntref_fmix32(0) == 0
+    for v in [1, 2, 0x12345678, 0xFFFFFFFF, 2891336453]:
+        assert O.ntref_fmix32(v) == fmix(v)
+    assert fmix(1) == 0x514E28B7  # widely published value of fmix32(1)
+
+
+def test_sample_position_random_texels():
+    """NT_SAMPLES_RANDOM: texel from fmix32 of the sample seed (twice), jitter from the
+    seed's first two uniforms (the mode's definition in nt.h), region fields ignored;
+    positions cover the image uniformly."""
+    W, H = 200, 120
+    st = P.TrainState([P.make_grid(8, 8, 1, 3)], P.make_network([3, 16, 16]), [], W, H,
+                      num_samples=4096, region_width=64, texel_offset_x=17, texel_offset_y=5,
+                      step=3, sample_mode=abi.NT_SAMPLES_RANDOM)
+    p = st.params()
+    uvz = (C.c_float * 3)()
+    xs, ys = [], []
+    for i in range(4096):
+        O.ntref_sample_uvz(C.byref(p), i, uvz)
+        seed = O.ntref_sample_seed(i, 3)
+        h1 = O.ntref_fmix32(seed)
+        h2 = O.ntref_fmix32(h1)
+        u0 = np.float32(h1 & 0xFFFFFF) * np.float32(2.0 ** -24)
+        u1 = np.float32(h2 & 0xFFFFFF) * np.float32(2.0 ** -24)
+        s = C.c_uint32(seed)
+        u2, u3 = O.ntref_uniform(C.byref(s)), O.ntref_uniform(C.byref(s))
+        x, y = min(int(np.float32(u0) * np.float32(W)), W - 1), min(int(np.float32(u1) * np.float32(H)), H - 1)
+        px = min(max(np.float32(x) + np.float32(0.5) + (np.float32(u2) - np.float32(0.5)), 0.5), W - 0.5)
+        py = min(max(np.float32(y) + np.float32(0.5) + (np.float32(u3) - np.float32(0.5)), 0.5), H - 0.5)
+        assert uvz[0] == np.float32(np.float32(px) / np.float32(W)), i
+        assert uvz[1] == np.float32(np.float32(py) / np.float32(H)), i
+        assert uvz[2] == 0.0
+        xs.append(x)
+        ys.append(y)
+    # Uniform over the image: every column band and row band is hit about equally.
+    cx = np.bincount(np.array(xs) * 10 // W, minlength=10)
+    cy = np.bincount(np.array(ys) * 10 // H, minlength=10)
+    assert cx.min() > 300 and cy.min() > 300
+
+
 # ---- latent bilinear sampling (train.cu:263-314) --------------------------------------
 
 def _lat(grids):
