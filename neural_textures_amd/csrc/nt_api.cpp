@@ -291,6 +291,12 @@ constexpr size_t kMaxLds = 160 * 1024;
 // Plan of the 16-channel kernel (nt_train16.hip): unconstrained latents of 16 channels,
 // one to four reference textures of the image size with float4 texels (their channels
 // become output rows 4t + ch), and an LDS layout that fits. Sets plan->use16.
+// 1/n when n is a power of two (exact in fp32), else 0.
+float pow2_reciprocal(int n)
+{
+    return n > 0 && (n & (n - 1)) == 0 ? 1.f / (float)n : 0.f;
+}
+
 void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
 {
     plan->use16 = 0;
@@ -299,6 +305,10 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     if (type != NT_UNCONSTRAINED || C != 16 || NG == 0 || p->num_textures < 1 || p->num_textures > 4 ||
         p->sample_mode != NT_SAMPLES_REGION)
         return;
+    // The prologue copies the weight matrices with 16-byte loads.
+    for (int l = 0; l < p->mlp.num_layers; ++l)
+        if (!aligned16(p->mlp.weights[l]))
+            return;
     Train16Desc &d = plan->t16;
     d = Train16Desc{};
     int prefix = 0;
@@ -314,6 +324,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         const int nch = x.num_channels < 4 ? x.num_channels : 4;
         d.tex[t] = x.texels + x.mip_offset[0] * 4;
         d.tex_nch[t] = nch;
+        d.four_channels |= nch == 4;
         d.tex_w[t] = x.loss_weight;
         for (int ch = 0; ch < nch; ++ch) {
             row_out[4 * t + ch] = (int8_t)(prefix + ch);
@@ -334,7 +345,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             row_out[r] = (int8_t)next;
             mapped[next] = true;
         }
-        d.perm[r] = row_out[r];
+        d.perm |= (uint64_t)row_out[r] << (4 * r);
     }
     d.ntex = p->num_textures;
     const int rw = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
@@ -394,14 +405,16 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         return;
     d.group_off = (int)((head + (size_t)fp * 4 + 15) & ~(size_t)15);
     const size_t lds = (size_t)d.group_off + (size_t)NG * d.group_bytes;
-    if (lds > kMaxLds)
+    // The prologue stages the fp16 weight matrices in the group regions.
+    if (lds > kMaxLds || train16_raw_bytes(plan->shape) > (size_t)NG * d.group_bytes)
         return;
     plan->use16 = 1;
     plan->groups = NG;
     plan->lds = lds;
     plan->nwg = d.nwg;
     plan->rows = d.nwg; // the groups of a workgroup merge their partials in LDS
-    plan->workspace = plan->weight_bytes + (size_t)plan->rows * (size_t)plan->P * sizeof(float);
+    plan->weight_bytes = 0; // each workgroup builds its weight image in LDS
+    plan->workspace = (size_t)plan->rows * (size_t)plan->P * sizeof(float);
     d.image_w = p->image_width;
     d.image_h = p->image_height;
     d.off_x = p->texel_offset_x;
@@ -409,6 +422,9 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     d.region_w = rw;
     d.num_samples = p->num_samples;
     d.step = (uint32_t)p->step;
+    d.inv_w = pow2_reciprocal(d.image_w);
+    d.inv_h = pow2_reciprocal(d.image_h);
+    d.inv_samples = pow2_reciprocal(d.num_samples);
 }
 
 int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
@@ -638,18 +654,9 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     float *partial = (float *)(ws + plan.weight_bytes);
     hipError_t e;
     if (plan.use16) {
-        Prep16Desc prep{};
-        prep.mlp = mlp_desc(&p->mlp);
-        memcpy(prep.perm, plan.t16.perm, sizeof(prep.perm));
-        prep.frags = (uint4 *)ws;
-        prep.bias = (float *)(ws + train_frag_bytes(plan.shape));
         Train16Desc d = plan.t16;
-        d.wfrags = prep.frags;
-        d.wbias = prep.bias;
+        d.mlp = mlp_desc(&p->mlp);
         d.partial = partial;
-        e = launch_prep16(plan.shape, prep, s);
-        if (e != hipSuccess)
-            return hip_status(e, "weight preparation launch");
         {
             ProfileScope prof(s);
             e = launch_train16(plan.shape, d, plan.lds, s);

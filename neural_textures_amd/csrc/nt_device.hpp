@@ -102,13 +102,23 @@ template <>
 struct RawWords<1> {
     using type = unsigned int;
 };
-// Load a 4-, 8- or 16-byte value from global memory.
+// Load a 2-, 4-, 8- or 16-byte value from global memory.
 template <class T>
 __device__ __forceinline__ T load_global(const T *p)
 {
     static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 16, "4, 8 or 16 bytes");
     using V = typename RawWords<sizeof(T) / 4>::type;
     return __builtin_bit_cast(T, *(global_ptr<V>)p);
+}
+__device__ __forceinline__ uint16_t load_global(const uint16_t *p) { return *(global_ptr<uint16_t>)p; }
+
+// x / d, as x * inv when inv (wave-uniform) is the exact reciprocal of a power of two d:
+// both are the correctly rounded value of the same real number.
+__device__ __forceinline__ float div_pow2(float x, float d, float inv)
+{
+    if (inv != 0.f)
+        return x * inv;
+    return x / d;
 }
 
 __device__ __forceinline__ _Float16 bits_h(uint16_t b) { return __builtin_bit_cast(_Float16, b); }

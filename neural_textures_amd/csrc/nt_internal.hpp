@@ -89,23 +89,19 @@ struct Train16Desc {
     int tex_nch[4];
     float tex_w[4];      // loss weight of texture t's rows
     int ntex;
+    int four_channels;   // some texture has four channels
     int image_w, image_h, off_x, off_y, region_w, num_samples;
     uint32_t step;
+    // 1/image_w, 1/image_h, 1/num_samples where that is a power of two (a product with the
+    // reciprocal then equals the quotient exactly), else 0 (divide).
+    float inv_w, inv_h, inv_samples;
     int tiles_x, ntiles, nwg, xcd_per; // xcd_per > 0: workgroups of one XCD take consecutive tiles
     int fp_floats;
     int group_off, group_bytes, tile_bytes; // per 4-wave group: target tile, then the union
     int wcols;                              // halves per scatter-weight row (one row per sample)
-    int8_t perm[NT_MAX_OUTPUTS];            // output index of output row r
-    const uint4 *wfrags;
-    const float *wbias;
+    uint64_t perm;                          // nibble r: output index of output row r
+    MlpDesc mlp;                            // fp16 weights and biases, read in the prologue
     float *partial; // [nwg][grad_total]
-};
-
-struct Prep16Desc {
-    MlpDesc mlp;
-    int8_t perm[NT_MAX_OUTPUTS];
-    uint4 *frags;
-    float *bias;
 };
 
 // Weight-fragment preparation (once per train step) for the train kernel.
@@ -275,7 +271,7 @@ int train16_groups(int shape);
 size_t train16_head_bytes(int shape);
 size_t train16_transpose_bytes(int shape);
 int train16_slots(int shape); // dW tiles per wave
-hipError_t launch_prep16(int shape, const Prep16Desc &d, hipStream_t s);
+size_t train16_raw_bytes(int shape); // fp16 weight matrices staged in the prologue
 hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream_t s);
 int train_grad_total(int shape);
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s);

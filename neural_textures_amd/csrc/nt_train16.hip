@@ -38,15 +38,81 @@ struct T16Layout {
     static constexpr int slots = (S::dw_total() + 3) / 4;
 };
 
-// ---- weight preparation ----------------------------------------------------------------
+// ---- weight preparation (the workgroup prologue) ----------------------------------------
+//
+// Each workgroup builds its LDS weight image itself from the fp16 weights: the matrices are
+// first staged in LDS as they lie in memory (W_l[n * kin + k], padded), the last layer's
+// rows already in output-row order, then read back as MFMA fragments. The image depends on
+// the weights only, so every workgroup builds the same one; there is no separate
+// preparation launch per step.
 
+// Half offset of layer l's matrix in the staged copy.
 template <class S>
-__device__ h8 weight_fragment16(const MlpDesc &m, const int8_t *perm, int idx)
+__host__ __device__ constexpr int raw_off(int l)
 {
-    const int f = idx / kWave, lane = idx % kWave, c = lane & 31, g = lane >> 5;
-    h8 v;
-    int l = 0;
+    int o = 0;
+    for (int j = 0; j < l; ++j)
+        o += S::kout(j) * S::kin(j);
+    return o;
+}
+
+// Output index of output row r (r < 16): nibble r of the packed permutation.
+__device__ __forceinline__ int perm_row(uint64_t perm, int r) { return (int)((perm >> (4 * r)) & 15u); }
+
+// Stage the weight matrices (16-byte loads; every matrix is a whole number of 16-byte
+// rows) and the fp32 bias rows. All global loads are issued before the first LDS store, so
+// the copy costs one memory round trip.
+template <class S, int NT>
+__device__ __forceinline__ void stage_weights16(const Train16Desc &d, uint16_t *raw, float *bias, int tid)
+{
+    constexpr int L = S::L;
+    static_assert(L <= 4, "train16 networks have at most four layers");
+    constexpr int I0 = (S::kout(0) * S::kin(0) / 8 + NT - 1) / NT;
+    constexpr int I1 = (S::kout(1) * S::kin(1) / 8 + NT - 1) / NT;
+    constexpr int I2 = L > 2 ? (S::kout(2) * S::kin(2) / 8 + NT - 1) / NT : 0;
+    constexpr int I3 = L > 3 ? (S::kout(3) * S::kin(3) / 8 + NT - 1) / NT : 0;
+    constexpr int it[4] = {I0, I1, I2, I3};
+    constexpr int first[4] = {0, I0, I0 + I1, I0 + I1 + I2};
+    uint4 v[I0 + I1 + I2 + I3 > 0 ? I0 + I1 + I2 + I3 : 1];
+    uint16_t bv[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const uint4 *W = (const uint4 *)d.mlp.W[l];
+        const int n4 = S::kout(l) * S::kin(l) / 8;
+        // Loads from clamped (always valid) addresses, so that none sits under a branch.
+#pragma unroll
+        for (int j = 0; j < it[l]; ++j)
+            v[first[l] + j] = load_global(W + min(tid + j * NT, n4 - 1));
+        // Bias row tid of layer l (output-row order on the last layer); 0 past the outputs.
+        const int n = l == L - 1 ? (tid < NT_MAX_OUTPUTS ? perm_row(d.perm, tid) : NT_MAX_OUTPUTS) : tid;
+        const uint16_t b = load_global(d.mlp.B[l] + min(n, d.mlp.sizes[l + 1] - 1));
+        bv[l] = n < d.mlp.sizes[l + 1] ? b : (uint16_t)0;
+    }
+    // Keeps the loads above the conditional stores below (the compiler would otherwise sink
+    // each load to its store and wait for it there).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int n4 = S::kout(l) * S::kin(l) / 8;
+        uint4 *dst = (uint4 *)(raw + raw_off<S>(l));
+#pragma unroll
+        for (int j = 0; j < it[l]; ++j) {
+            const int i = tid + j * NT;
+            if (i < n4)
+                dst[i] = v[first[l] + j];
+        }
+        if (tid < 32 * S::t32(S::kout(l)))
+            bias[S::bias_off(l) + tid] = h2f(bv[l]);
+    }
+}
+
+// Fragment f (wave-uniform) for lane (c, g), read from the staged matrices.
+template <class S>
+__device__ __forceinline__ h8 weight_fragment16(const uint16_t *raw, uint64_t perm, int f, int lane)
+{
+    const int c = lane & 31, g = lane >> 5;
     const bool fwd = f < S::fwd_total();
+    int l = 0;
     if (fwd) {
         while (l + 1 < S::L && f >= S::fwd_off(l + 1))
             ++l;
@@ -56,21 +122,30 @@ __device__ h8 weight_fragment16(const MlpDesc &m, const int8_t *perm, int idx)
     }
     const int kin = S::kin(l), kout = S::kout(l);
     const bool last = l == S::L - 1;
-    const uint16_t *W = m.W[l];
+    const uint16_t *W = raw + raw_off<S>(l);
+    h8 v;
     if (fwd) {
-        // Forward fragment (a, q): A[row][kk] = W_l[n][k], row = 32a + c, n = the output of
-        // that row (permuted on the last layer), k = the input of (q, g, e).
+        // Forward fragment (a, q): A[row][kk] = W_l[n][k], row = 32a + c, n the output of that
+        // row (permuted on the last layer), k = the input of (q, g, e): eight consecutive
+        // inputs on layer 0, two runs of four on the others.
         const int local = f - S::fwd_off(l), qn = kin / 16;
         const int a = local / qn, q = local % qn;
         const int row = 32 * a + c;
-        const int n = last ? (row < NT_MAX_OUTPUTS ? perm[row] : kout) : row;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int k = l == 0 ? grid_feature(q, g, e) : chained_feature(q, g, e);
-            v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+        if (row < kout) {
+            const int n = last ? perm_row(perm, row) : row;
+            const uint16_t *wr = W + n * kin;
+            if (l == 0) {
+                v = *(const h8 *)(wr + grid_feature(q, g, 0));
+            } else {
+                const h4 lo = *(const h4 *)(wr + chained_feature(q, g, 0));
+                const h4 hi = *(const h4 *)(wr + chained_feature(q, g, 4));
+                v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        } else {
+            v = (h8)(_Float16)0.f;
         }
     } else {
-        // Backward fragment (mt, q): A[k][kk] = W_l[n][k], k = 32mt + c, n = the output of
+        // Backward fragment (mt, q): A[k][kk] = W_l[n][k], k = 32mt + c, n the output of the
         // chained row (q, g, e).
         const int local = f - S::bwd_off(l), qn = kout / 16;
         const int mt = local / qn, q = local % qn;
@@ -78,36 +153,11 @@ __device__ h8 weight_fragment16(const MlpDesc &m, const int8_t *perm, int idx)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int row = chained_feature(q, g, e);
-            const int n = last ? perm[row] : row;
-            v[e] = (n < kout && k < kin) ? bits_h(W[n * kin + k]) : (_Float16)0.f;
+            const int n = last ? perm_row(perm, row) : row;
+            v[e] = k < kin ? bits_h(W[n * kin + k]) : (_Float16)0.f;
         }
     }
     return v;
-}
-
-template <class S>
-__device__ float bias_value16(const MlpDesc &m, const int8_t *perm, int idx)
-{
-    int l = 0;
-    while (l + 1 < S::L && idx >= S::bias_off(l + 1))
-        ++l;
-    int n = idx - S::bias_off(l);
-    if (l == S::L - 1) {
-        if (n >= NT_MAX_OUTPUTS)
-            return 0.f;
-        n = perm[n];
-    }
-    return n < m.sizes[l + 1] ? h2f(m.B[l][n]) : 0.f;
-}
-
-template <class S>
-__global__ __launch_bounds__(256) void prep16_kernel(Prep16Desc d)
-{
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < S::all_frags() * kWave)
-        d.frags[i] = __builtin_bit_cast(uint4, weight_fragment16<S>(d.mlp, d.perm, i));
-    if (i < S::bias_total())
-        d.bias[i] = bias_value16<S>(d.mlp, d.perm, i);
 }
 
 // ---- device pieces ---------------------------------------------------------------------
@@ -121,27 +171,46 @@ __device__ __forceinline__ h4 lds_read_tr16(const _Float16 *p)
 
 // Start the copy of the chunk's target tile (texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of
 // every texture, wrapped like the reference's texture objects, main.cpp:613-621) into the
-// group's LDS tile with global_load_lds_dwordx4: per texture, wave w copies texels
-// 64(w + 4k) + lane, each wave instruction filling 64 consecutive float4 slots. No
+// group's LDS tile with global_load_lds_dwordx4: wave w copies texels 64(w + 4k) + lane of
+// each texture, each wave instruction filling 64 consecutive float4 slots. No
 // registers are held; the caller waits for vmcnt(0) before the barrier that publishes it.
 __device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *tile, int cx0, int cy0,
                                                  int wave, int lane)
 {
-    for (int t = 0; t < d.ntex; ++t) {
-        const float *tex = d.tex[t];
-        float4 *dst = tile + t * kTileTexels;
-        for (int base = 64 * wave; base < kTileTexels; base += 64 * 4) {
-            const int i = base + lane;
-            if (i < kTileTexels) {
-                const int ty = i / kTileW, tx = i - ty * kTileW;
-                int gx = cx0 - kTileX0 + tx, gy = cy0 - kTileX0 + ty;
-                gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
-                gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
-                __builtin_amdgcn_global_load_lds((const void *)(tex + ((int64_t)gy * d.image_w + gx) * 4),
-                                                 (__attribute__((address_space(3))) void *)(dst + base), 16, 0, 0);
-            }
+    for (int base = 64 * wave; base < kTileTexels; base += 64 * 4) {
+        const int i = base + lane;
+        if (i < kTileTexels) {
+            const int ty = i / kTileW, tx = i - ty * kTileW;
+            int gx = cx0 - kTileX0 + tx, gy = cy0 - kTileX0 + ty;
+            gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
+            gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
+            const int64_t off = ((int64_t)gy * d.image_w + gx) * 4; // same texel of every texture
+            for (int t = 0; t < d.ntex; ++t)
+                __builtin_amdgcn_global_load_lds((const void *)(d.tex[t] + off),
+                                                 (__attribute__((address_space(3))) void *)(tile + t * kTileTexels + base),
+                                                 16, 0, 0);
         }
     }
+}
+
+// The 16 Catmull-Rom taps of one texture from the LDS tile, fp32 fma in tap order; the
+// fourth channel only where some texture has one.
+template <bool FOUR>
+__device__ __forceinline__ void cr_taps(const float4 *base, const float (&wx)[4], const float (&wy)[4],
+                                        float (&acc)[4])
+{
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 p = base[jj * kTileW + i];
+            const float wxy = wx[i] * wy[jj];
+            acc[0] = fmaf(p.x, wxy, acc[0]);
+            acc[1] = fmaf(p.y, wxy, acc[1]);
+            acc[2] = fmaf(p.z, wxy, acc[2]);
+            if (FOUR)
+                acc[3] = fmaf(p.w, wxy, acc[3]);
+        }
 }
 
 // Catmull-Rom targets and loss weights of the lane's eight output rows 8j + 4g + ch,
@@ -162,17 +231,10 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
         if (ti < d.ntex) {
             if (inside) {
                 const float4 *base = tile + ti * kTileTexels + y0 * kTileW + x0;
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float4 p = base[jj * kTileW + i];
-                        const float wxy = wx[i] * wy[jj];
-                        acc[0] = fmaf(p.x, wxy, acc[0]);
-                        acc[1] = fmaf(p.y, wxy, acc[1]);
-                        acc[2] = fmaf(p.z, wxy, acc[2]);
-                        acc[3] = fmaf(p.w, wxy, acc[3]);
-                    }
+                if (d.four_channels)
+                    cr_taps<true>(base, wx, wy, acc);
+                else
+                    cr_taps<false>(base, wx, wy, acc);
             } else {
                 const float *tex = g ? sreg(d.tex[2 * j + 1]) : sreg(d.tex[2 * j]);
                 for (int jj = 0; jj < 4; ++jj) {
@@ -273,15 +335,18 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     _Float16 *wlo = whi + kChunk * d.wcols;   // ... lo
 
     {
-        const uint4 *src = d.wfrags;
-        uint4 *dst = (uint4 *)frags;
-        for (int i = tid; i < S::all_frags() * kWave; i += kTrainThreads * NG)
-            dst[i] = src[i];
-        for (int i = tid; i < S::bias_total(); i += kTrainThreads * NG)
-            bias[i] = d.wbias[i];
+        // Weight image (staged through the group regions, which the tile loop overwrites only
+        // after the barriers below), biases, and the cleared footprint box.
+        constexpr int NT = kTrainThreads * NG;
+        uint16_t *raw = (uint16_t *)(smem + d.group_off);
+        stage_weights16<S, NT>(d, raw, bias, tid);
         float4 *f4 = (float4 *)fp;
-        for (int i = tid; i < d.fp_floats / 4; i += kTrainThreads * NG)
+        for (int i = tid; i < d.fp_floats / 4; i += NT)
             f4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        __syncthreads();
+        for (int f = __builtin_amdgcn_readfirstlane(tid >> 6); f < S::all_frags(); f += NT / kWave)
+            frags[f * kWave + lane] = weight_fragment16<S>(raw, d.perm, f, lane);
+        __syncthreads();
     }
 
     f16v dwacc[LY::slots];
@@ -324,8 +389,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         const float jy = uniform01(st) - 0.5f;
         const float px = clampf((float)(uint32_t)(d.off_x + sx) + 0.5f + jx, 0.5f, (float)d.image_w - 0.5f);
         const float py = clampf((float)(uint32_t)(d.off_y + sy) + 0.5f + jy, 0.5f, (float)d.image_h - 0.5f);
-        const float u = px / (float)d.image_w;
-        const float v = py / (float)d.image_h;
+        const float u = div_pow2(px, (float)d.image_w, d.inv_w);
+        const float v = div_pow2(py, (float)d.image_h, d.inv_h);
 
         h8 x0[KQ0];
         if (valid) {
@@ -359,13 +424,26 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         {
             float tgt[8], tw[8];
             lane_targets16(d, tile, cx0, cy0, u, v, g, tgt, tw);
+            float grd[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float y = (float)(_Float16)out[0][e];
-                const float err = y - tgt[e];
-                const float grd = 2.f * tw[e] * err / (float)d.num_samples;
-                dyo[0][e] = valid ? (_Float16)grd : (_Float16)0.f;
+                grd[e] = 2.f * tw[e] * (y - tgt[e]);
             }
+            // One uniform branch: the product with the exact reciprocal of a power-of-two N,
+            // else the quotient.
+            if (d.inv_samples != 0.f) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    grd[e] *= d.inv_samples;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    grd[e] /= (float)d.num_samples;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                dyo[0][e] = valid ? (_Float16)grd[e] : (_Float16)0.f;
         }
 
         // ---- backward, last layer (mlp.h:302-362)
@@ -585,7 +663,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                 const int row = 32 * a + 8 * (e >> 2) + 4 * g + (e & 3);
                 const int k = 32 * bb + c;
                 if (row < kout && k < kin) {
-                    const int n = l == L - 1 ? d.perm[row] : row;
+                    const int n = l == L - 1 ? perm_row(d.perm, row) : row;
                     part[off + n * kin + k] = dwacc[j][e];
                 }
             }
@@ -595,7 +673,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     for (int l = 0; l < L; ++l)
         if (t256 < 4 * S::kout(l) && (t256 & 3) == 0) {
             const int row = t256 >> 2;
-            const int n = l == L - 1 ? d.perm[row] : row;
+            const int n = l == L - 1 ? perm_row(d.perm, row) : row;
             part[S::grad_off(l) + S::kout(l) * S::kin(l) + n] = dbacc[l];
         }
 }
@@ -649,6 +727,18 @@ int train16_slots(int shape)
     }
 }
 
+size_t train16_raw_bytes(int shape)
+{
+    switch (shape) {
+    case kShapeC2:
+        return raw_off<ShapeC2>(ShapeC2::L) * 2;
+    case kShapeC4:
+        return raw_off<ShapeC4>(ShapeC4::L) * 2;
+    default:
+        return 0;
+    }
+}
+
 size_t train16_transpose_bytes(int shape)
 {
     switch (shape) {
@@ -658,26 +748,6 @@ size_t train16_transpose_bytes(int shape)
         return TrainLayout<ShapeC4>::transpose_bytes;
     default:
         return 0;
-    }
-}
-
-template <class S>
-static hipError_t prep16(const Prep16Desc &d, hipStream_t s)
-{
-    const int n = S::all_frags() * kWave > S::bias_total() ? S::all_frags() * kWave : S::bias_total();
-    hipLaunchKernelGGL(prep16_kernel<S>, dim3((n + 255) / 256), dim3(256), 0, s, d);
-    return hipGetLastError();
-}
-
-hipError_t launch_prep16(int shape, const Prep16Desc &d, hipStream_t s)
-{
-    switch (shape) {
-    case kShapeC2:
-        return prep16<ShapeC2>(d, s);
-    case kShapeC4:
-        return prep16<ShapeC4>(d, s);
-    default:
-        return hipErrorInvalidValue;
     }
 }
 
