@@ -40,12 +40,16 @@ __global__ __launch_bounds__(256) void net_adam_kernel(NetAdamDesc d)
         // OptimizePaddedParameterMatrix (train.cu:590-623): active rows x cols only.
         const int row = local % d.rows[l], col = local / d.rows[l];
         const int idx = col * d.pin[l] + row;
+        // Network gradients are almost all non-zero: the moments and the weight are loaded
+        // with the gradient, in one round trip.
         float *gp = d.g[l] + idx;
         const float g = *gp;
+        float m1 = d.m1[l][idx], m2 = d.m2[l][idx];
+        const uint16_t wb = d.w[l][idx];
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // keeps the loads above the test
         if (g == 0.f)
             return;
-        float m1 = d.m1[l][idx], m2 = d.m2[l][idx];
-        const float w = adam_update(m1, m2, g, d.a, h2f(d.w[l][idx]));
+        const float w = adam_update(m1, m2, g, d.a, h2f(wb));
         d.m1[l][idx] = m1;
         d.m2[l][idx] = m2;
         d.w[l][idx] = h_bits((_Float16)w);
@@ -55,10 +59,12 @@ __global__ __launch_bounds__(256) void net_adam_kernel(NetAdamDesc d)
         const int idx = local - nw;
         float *gp = d.bg[l] + idx;
         const float g = *gp;
+        float m1 = d.bm1[l][idx], m2 = d.bm2[l][idx];
+        const uint16_t bb = d.b[l][idx];
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (g == 0.f)
             return;
-        float m1 = d.bm1[l][idx], m2 = d.bm2[l][idx];
-        const float w = adam_update(m1, m2, g, d.a, h2f(d.b[l][idx]));
+        const float w = adam_update(m1, m2, g, d.a, h2f(bb));
         d.bm1[l][idx] = m1;
         d.bm2[l][idx] = m2;
         d.b[l][idx] = h_bits((_Float16)w);

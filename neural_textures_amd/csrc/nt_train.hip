@@ -896,12 +896,13 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 
 // Two-stage deterministic reduction of the per-workgroup partials into the network
 // gradients (which the contract says are accumulated into, train.cu:1028-1048).
-// partial[rows][P] -> the MLP gradients, in one pass and a fixed order: a workgroup owns 16
-// parameters and splits the rows into 16 contiguous groups, one per 16-lane slice; each
-// lane sums its group's rows in row order (all loads issued before the adds), then lane
-// group 0 adds the 16 group sums in group order. The same bits on every run.
-constexpr int kReduceCols = 16, kReduceGroups = 16, kReduceUnroll = 16;
-__global__ __launch_bounds__(256) void reduce_rows(ReduceDesc d)
+// partial[rows][P] -> the MLP gradients, in one pass and a fixed order: a workgroup owns 64
+// parameters and splits the rows into 16 contiguous groups, one per wave; each lane sums its
+// group's rows of one parameter in row order (all loads issued before the adds: every wave
+// load is 256 contiguous bytes of one row), then wave 0 adds the 16 group sums in group
+// order. The same bits on every run.
+constexpr int kReduceCols = 64, kReduceGroups = 16, kReduceUnroll = 16;
+__global__ __launch_bounds__(kReduceCols *kReduceGroups) void reduce_rows(ReduceDesc d)
 {
     __shared__ float part[kReduceGroups][kReduceCols];
     const int col = threadIdx.x % kReduceCols, grp = threadIdx.x / kReduceCols;
@@ -965,7 +966,8 @@ static hipError_t launch_prep(const PrepDesc &d, hipStream_t s)
 
 hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s)
 {
-    hipLaunchKernelGGL(reduce_rows, dim3((d.P + kReduceCols - 1) / kReduceCols), dim3(256), 0, s, d);
+    hipLaunchKernelGGL(reduce_rows, dim3((d.P + kReduceCols - 1) / kReduceCols), dim3(kReduceCols * kReduceGroups), 0,
+                       s, d);
     return hipGetLastError();
 }
 

@@ -584,29 +584,23 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 
     __syncthreads();
     // ---- flush the footprint box with global float atomics, clearing it for the next tile
-    // (the next tile's first box access follows at least one barrier)
+    // (the next tile's first box access follows at least one barrier). Lane i takes float i,
+    // so one atomic instruction covers 64 consecutive floats (four texels) of the gradient
+    // array: four full 64-byte lines per instruction.
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
         const Grid16 &q = d.grid[gi];
-        float4 *box = (float4 *)(fp + q.fp_off);
-        const int n4 = q.fp_w * q.fp_h * 4;
-        for (int i = tid; i < n4; i += kTrainThreads * NG) {
-            const float4 val = box[i];
-            if (val.x == 0.f && val.y == 0.f && val.z == 0.f && val.w == 0.f)
+        float *box = fp + q.fp_off;
+        const int n = q.fp_w * q.fp_h * 16;
+        for (int i = tid; i < n; i += kTrainThreads * NG) {
+            const float val = box[i];
+            if (val == 0.f)
                 continue;
-            box[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            const int cell = i >> 2, part = i & 3;
+            box[i] = 0.f;
+            const int cell = i >> 4, ch = i & 15;
             const int ly = (int)(((float)cell + 0.5f) * q.inv_fp_w), lx = cell - ly * q.fp_w;
             const int gx = wrap_near(flo_x[gi] + lx, q.w), gy = wrap_near(flo_y[gi] + ly, q.h);
-            float *dst = q.grads + ((int64_t)gy * q.w + gx) * 16 + 4 * part;
-            if (val.x != 0.f)
-                global_add(dst, val.x);
-            if (val.y != 0.f)
-                global_add(dst + 1, val.y);
-            if (val.z != 0.f)
-                global_add(dst + 2, val.z);
-            if (val.w != 0.f)
-                global_add(dst + 3, val.w);
+            global_add(q.grads + ((int64_t)gy * q.w + gx) * 16 + ch, val);
         }
     }
     } // tiles
