@@ -445,6 +445,60 @@ __device__ __forceinline__ void scatter_unconstrained(const TrainDesc &d, const 
         }
 }
 
+// Latent gradient scatter without a footprint box, 16 channels (train.cu:460-509, the
+// same adds): the wave stages its 32 samples' dX0 rows and bilinear corners (texel index,
+// weight) in its own LDS slice, then walks the samples with lane = 16 * corner + channel,
+// so one atomic instruction adds whole 64-byte texel records instead of 64 scattered
+// floats. Called with all lanes of the wave; invalid samples have no corners.
+template <int KQ, int GM>
+struct Rows16 {
+    static constexpr int K0 = KQ * 16;
+    static constexpr int dx_bytes = 32 * K0 * 2;
+    static constexpr int bytes = dx_bytes + 32 * GM * 4 * 8; // + texel index, weight per corner
+};
+
+template <int KQ, int GM>
+__device__ __forceinline__ void scatter_rows16(const TrainDesc &d, const SampleFootprints &f, const h8 (&dx)[KQ],
+                                               bool valid, int lane, unsigned char *slice)
+{
+    using R = Rows16<KQ, GM>;
+    const int c = lane & 31, g = lane >> 5;
+    _Float16 *dxr = (_Float16 *)slice;
+    int *cidx = (int *)(slice + R::dx_bytes);
+    float *cw = (float *)(cidx + 32 * GM * 4);
+    // Chained fragment q of lane group g holds features 16q + 4g + (0..3) and 16q + 8 + 4g + (0..3).
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) {
+        *(h4 *)(dxr + c * R::K0 + 16 * q + 4 * g) = __builtin_shufflevector(dx[q], dx[q], 0, 1, 2, 3);
+        *(h4 *)(dxr + c * R::K0 + 16 * q + 8 + 4 * g) = __builtin_shufflevector(dx[q], dx[q], 4, 5, 6, 7);
+    }
+    // Lane group g records corners 2g and 2g + 1 of every grid.
+#pragma unroll
+    for (int gi = 0; gi < GM; ++gi) {
+        const GridDesc &gr = d.grid[gi];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int k = 2 * g + kk;
+            const int tx = f.x0[gi] + kk, ty = f.y0[gi] + g;
+            const int slot = (c * GM + gi) * 4 + k;
+            cidx[slot] = valid ? wrap_near(ty, gr.h) * gr.w + wrap_near(tx, gr.w) : -1;
+            cw[slot] = g ? f.w[gi][2 + kk] : f.w[gi][kk];
+        }
+    }
+    const int k = lane >> 4, ch = lane & 15;
+#pragma unroll 4
+    for (int s = 0; s < 32; ++s) {
+#pragma unroll
+        for (int gi = 0; gi < GM; ++gi) {
+            const int slot = (s * GM + gi) * 4 + k;
+            const int idx = cidx[slot];
+            const float gv = (float)dxr[s * R::K0 + 16 * gi + ch];
+            if (idx >= 0 && gv != 0.f)
+                global_add(d.grid[gi].grads + (int64_t)idx * 16 + ch, cw[slot] * gv);
+        }
+    }
+}
+
 // BC6 backward of one sample (train.cu:373-458), straight to global atomics.
 template <int C, int KQ>
 __device__ __forceinline__ void scatter_bc6(const TrainDesc &d, const SampleFootprints &f,
@@ -815,6 +869,11 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
                     __syncthreads();
                     scatter_reduce<S, C, GM>(d, cbx, cby, flo_x, flo_y, fp, sct, 0, wave, lane);
                     __syncthreads();
+                } else if (!mfma_scatter && d.fp_floats == 0) {
+                    static_assert(4 * Rows16<KQ0, GM>::bytes <= LY::transpose_bytes, "row slices fit the union");
+                    scatter_rows16<KQ0, GM>(d, fps, dx0, valid, lane, un + wave * Rows16<KQ0, GM>::bytes);
+                    if (d.tile_ok)
+                        __syncthreads(); // the next chunk's target tile reuses the union
                 } else if (!mfma_scatter && valid) {
                     scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
                 }
