@@ -261,10 +261,10 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
     }
 }
 
-// Bilinear footprint of grid gi at mip 0 (train.cu:284-303, z = 0).
-__device__ __forceinline__ Footprint footprint16(const Grid16 &gr, float u, float v)
+// Bilinear footprint at mip 0 of a w x h grid (train.cu:284-303, z = 0).
+__device__ __forceinline__ Footprint footprint16(int w, int h, float u, float v)
 {
-    return bilinear_footprint(u, v, gr.w, gr.h, 1.f);
+    return bilinear_footprint(u, v, w, h, 1.f);
 }
 
 // Gather grids g + 2j of the lane into fragments 2j (channels 0-7) and 2j + 1 (8-15);
@@ -486,45 +486,49 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         __syncthreads();
 
         // ---- latent scatter (train.cu:460-509) as an MFMA reduction over the chunk
-        // Part 1: dX0^T, this sample's weight row (own entries cleared first), and corners
-        // outside the chunk cell box straight into the footprint box.
+        // Part 1: dX0^T; lane group g fills the weight-row entries of grids g, g + 2 for its
+        // sample (own entries cleared first). A footprint not wholly inside the chunk cell
+        // box (not expected: the box covers every corner a chunk position can reach, up to
+        // fp32 rounding) goes straight into the footprint box or global memory, all 16
+        // channels read back from dX0^T.
         store_transposed<KQ0, true>(dxt, dx0, col, g);
         {
             _Float16 *rhi = whi + col * d.wcols, *rlo = wlo + col * d.wcols;
-            const float ru = rn32(u), rv = rn32(v);
 #pragma unroll
-            for (int gi = 0; gi < G; ++gi) {
-                const Grid16 &q = d.grid[gi];
-                const int bx = (int)floorf(fmaf((float)cx0, q.rx, -0.5f));
-                const int by = (int)floorf(fmaf((float)cy0, q.ry, -0.5f));
-                const Footprint f = footprint16(q, ru, rv);
-                if ((gi & 1) == g) { // lane group g owns grids g, g + 2 of the weight row
-                    uint4 *zh = (uint4 *)(rhi + q.wcol0), *zl = (uint4 *)(rlo + q.wcol0);
-                    for (int k = 0; k < (q.ncell + 15) / 16 * 2; ++k) {
-                        zh[k] = make_uint4(0u, 0u, 0u, 0u);
-                        zl[k] = make_uint4(0u, 0u, 0u, 0u);
-                    }
+            for (int j = 0; j < G / 2; ++j) {
+                const Grid16 &qa = d.grid[2 * j], &qb = d.grid[2 * j + 1];
+                const int gi = 2 * j + g;
+                const int w = g ? qb.w : qa.w, h = g ? qb.h : qa.h;
+                const int cb_w = g ? qb.cb_w : qa.cb_w, cb_h = g ? qb.cb_h : qa.cb_h;
+                const int ncell = g ? qb.ncell : qa.ncell, wcol0 = g ? qb.wcol0 : qa.wcol0;
+                const float rx = g ? qb.rx : qa.rx, ry = g ? qb.ry : qa.ry;
+                const int bx = (int)floorf(fmaf((float)cx0, rx, -0.5f));
+                const int by = (int)floorf(fmaf((float)cy0, ry, -0.5f));
+                const Footprint f = footprint16(w, h, u, v);
+                uint4 *zh = (uint4 *)(rhi + wcol0), *zl = (uint4 *)(rlo + wcol0);
+                for (int k = 0; k < (ncell + 15) / 16 * 2; ++k) {
+                    zh[k] = make_uint4(0u, 0u, 0u, 0u);
+                    zl[k] = make_uint4(0u, 0u, 0u, 0u);
                 }
+                const int cx = f.x0 - bx, cy = f.y0 - by;
+                const bool inside = cx >= 0 && cx + 1 < cb_w && cy >= 0 && cy + 1 < cb_h;
+                if (valid && inside) {
 #pragma unroll
-                for (int corner = 0; corner < 4; ++corner) {
-                    const int tx = f.x0 + (corner & 1), ty = f.y0 + (corner >> 1);
-                    const int cx = tx - bx, cy = ty - by;
-                    const float w = f.w[corner];
-                    if (cx >= 0 && cx < q.cb_w && cy >= 0 && cy < q.cb_h) {
-                        if (valid && (gi & 1) == g) {
-                            const int k = q.wcol0 + cy * q.cb_w + cx;
-                            const _Float16 hi = (_Float16)w;
-                            rhi[k] = hi;
-                            rlo[k] = (_Float16)(w - (float)hi);
-                        }
-                    } else if (valid) {
-                        // This lane's dX0 channels of grid gi are rows chained(gi, g, e).
-                        const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
+                    for (int corner = 0; corner < 4; ++corner) {
+                        const int k = wcol0 + (cy + (corner >> 1)) * cb_w + cx + (corner & 1);
+                        const _Float16 hi = (_Float16)f.w[corner];
+                        rhi[k] = hi;
+                        rlo[k] = (_Float16)(f.w[corner] - (float)hi);
+                    }
+                } else if (valid) {
+                    const Grid16 &q = g ? qb : qa;
+                    const int lox = g ? flo_x[2 * j + 1] : flo_x[2 * j], loy = g ? flo_y[2 * j + 1] : flo_y[2 * j];
+                    for (int corner = 0; corner < 4; ++corner) {
+                        const int tx = f.x0 + (corner & 1), ty = f.y0 + (corner >> 1);
+                        const int lx = tx - lox, ly = ty - loy;
                         const bool inbox = lx >= 0 && lx < q.fp_w && ly >= 0 && ly < q.fp_h;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const int ch = chained_feature(0, g, e);
-                            const float val = w * (float)dx0[gi][e];
+                        for (int ch = 0; ch < 16; ++ch) {
+                            const float val = f.w[corner] * (float)dxt[(16 * gi + ch) * kRowStride + col];
                             if (inbox)
                                 lds_add(fp + q.fp_off + (ly * q.fp_w + lx) * 16 + ch, val);
                             else
