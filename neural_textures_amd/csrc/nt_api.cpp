@@ -394,13 +394,13 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     d.fp_floats = fp;
     d.wcols = wcols;
     const size_t head = train16_head_bytes(plan->shape);
-    const size_t scatter = ((size_t)p->mlp.sizes[0] * kRowStride + 2 * (size_t)kChunk * wcols) * 2;
+    const size_t scatter = ((size_t)kChunk * dx_stride(p->mlp.sizes[0]) + 2 * (size_t)kChunk * wcols) * 2;
     size_t un = train16_transpose_bytes(plan->shape);
     un = scatter > un ? scatter : un;
     d.tile_bytes = d.ntex * kTileW * kTileH * 16;
     d.group_bytes = (int)((d.tile_bytes + un + 15) & ~(size_t)15);
     // The second group's region carries its dW accumulators to the first at the end.
-    const size_t handoff = ((size_t)train16_slots(plan->shape) * 16 + (size_t)p->mlp.num_layers) * kTrainThreads * 4;
+    const size_t handoff = (size_t)train16_slots(plan->shape) * 17 * kTrainThreads * 4;
     if (NG == 2 && (size_t)d.group_bytes < handoff)
         return;
     d.group_off = (int)((head + (size_t)fp * 4 + 15) & ~(size_t)15);

@@ -18,6 +18,10 @@ constexpr int kChunkH = 8;
 constexpr int kChunk = kChunkW * kChunkH;
 constexpr int kTrainThreads = 256;
 constexpr int kRowStride = kChunk + 8; // fp16 row stride of the LDS transposes
+constexpr int kFeatStride = 72;         // fp16 row stride of the 16-channel kernel's sample rows
+// ... and of its dX0 rows (k0 inputs): 16 halves of padding put the four rows of one
+// transposed read in different LDS banks.
+__host__ __device__ constexpr int dx_stride(int k0) { return k0 + 16; }
 // Catmull-Rom target tile of one chunk: texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of every
 // reference texture, float4 each (covers all 16 taps of every jittered sample of the chunk).
 constexpr int kTileX0 = 3;

@@ -310,6 +310,107 @@ __device__ __forceinline__ void store_inputs_transposed(_Float16 *buf, const h8 
             buf[grid_feature(q, g, e) * kRowStride + col] = v[q][e];
 }
 
+// ---- sample-row tiles for the dW products --------------------------------------------------
+//
+// The group's layer inputs and output gradients are stored as sample rows
+// ([sample][kFeatStride] fp16: 8-byte stores of the chained runs of four features) and read
+// back transposed with ds_read_b64_tr_b16, which hands each lane of a 16-lane group four
+// consecutive samples of one feature: the K-major operands of dW = X^T dY.
+
+// Chained fragments q of the lane's sample: features 16q + 4g + (0..3), 16q + 8 + 4g + (0..3).
+template <int NQ, int STRIDE = kFeatStride>
+__device__ __forceinline__ void store_rows(_Float16 *buf, const h8 (&v)[NQ], int col, int g)
+{
+    _Float16 *row = buf + col * STRIDE + 4 * g;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        *(h4 *)(row + 16 * q) = __builtin_shufflevector(v[q], v[q], 0, 1, 2, 3);
+        *(h4 *)(row + 16 * q + 8) = __builtin_shufflevector(v[q], v[q], 4, 5, 6, 7);
+    }
+}
+
+// Layer-0 inputs in grid_feature order: eight consecutive features per fragment.
+template <int G>
+__device__ __forceinline__ void store_input_rows(_Float16 *buf, const h8 (&v)[G], int col, int g)
+{
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+        *(h8 *)(buf + col * kFeatStride + grid_feature(q, g, 0)) = v[q];
+}
+
+// Samples s0 .. s0 + 7 of feature f0 + i16 (i16 = lane within its 16-lane group; s0 and f0
+// uniform over the group) from rows of STRIDE halves.
+template <int STRIDE = kFeatStride>
+__device__ __forceinline__ h8 read_cols8(const _Float16 *buf, int s0, int f0, int i16)
+{
+    const _Float16 *p = buf + (s0 + (i16 >> 2)) * STRIDE + f0 + 4 * (i16 & 3);
+    const h4 a = lds_read_tr16(p), b = lds_read_tr16(p + 4 * STRIDE);
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// dW += X^T dY over the group's 128 samples for the dW tiles this wave owns (mlp.h:101-220).
+// A tile (a, 0) also sums its A operand (the output gradient of feature 32a + c over the
+// lane group's samples) into the tile's bias accumulator: fp32 sums of fp16 values, two per
+// v_dot2_f32_f16.
+template <class S, int l>
+__device__ __forceinline__ void dw_rows(const _Float16 *xs, const _Float16 *dys, f16v (&acc)[T16Layout<S, 1>::slots],
+                                        float (&db)[T16Layout<S, 1>::slots], int wave, int lane)
+{
+    constexpr int kin = S::kin(l), kout = S::kout(l);
+    constexpr int KB = S::t32(kin), NA = S::t32(kout);
+    constexpr int start = S::dw_start(l), ntiles = NA * KB;
+    const int c = lane & 31, g = lane >> 5, i16 = lane & 15, half = 16 * (c >> 4);
+    const h2 one = {(_Float16)1.f, (_Float16)1.f};
+#pragma unroll
+    for (int j = 0; j < T16Layout<S, 1>::slots; ++j) {
+        const int t = 4 * j + wave - start;
+        if (t >= 0 && t < ntiles) {
+            const int a = t / KB, b = t % KB;
+            const bool arow = 32 * a + c < kout, brow = 32 * b + c < kin;
+#pragma unroll
+            for (int q = 0; q < kChunk / 16; ++q) {
+                h8 A = read_cols8(dys, 16 * q + 8 * g, 32 * a + half, i16);
+                h8 B = read_cols8(xs, 16 * q + 8 * g, 32 * b + half, i16);
+                if (!arow)
+                    A = (h8)(_Float16)0.f;
+                if (!brow)
+                    B = (h8)(_Float16)0.f;
+                acc[j] = mfma32(A, B, acc[j]);
+                if (b == 0) {
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const h2 pair = {A[e], A[e + 1]};
+                        db[j] = __builtin_amdgcn_fdot2(pair, one, db[j], false);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Backward through hidden layer l (its input is hidden activation l-1), then l-1 ... 1.
+template <class S, int l>
+__device__ __forceinline__ void backward_hidden_rows(_Float16 *xs, _Float16 *dys, const h8 *frags,
+                                                     const h8 (&xh)[S::NH][S::H / 16], h8 (&dyh)[S::H / 16],
+                                                     f16v (&dwacc)[T16Layout<S, 1>::slots],
+                                                     float (&dbt)[T16Layout<S, 1>::slots], int col, int wave,
+                                                     int lane)
+{
+    if constexpr (l >= 1) {
+        constexpr int HQ = S::H / 16, HA = S::t32(S::H);
+        const int g = lane >> 5;
+        store_rows<HQ>(dys, dyh, col, g);
+        store_rows<HQ>(xs, xh[l - 1], col, g);
+        f16v acc[HA];
+        layer_backward_dx<HQ, HA>(frags + S::bwd_off(l) * kWave, dyh, acc, lane);
+        relu_backward<HQ, HA>(acc, xh[l - 1], dyh);
+        __syncthreads();
+        dw_rows<S, l>(xs, dys, dwacc, dbt, wave, lane);
+        __syncthreads();
+        backward_hidden_rows<S, l - 1>(xs, dys, frags, xh, dyh, dwacc, dbt, col, wave, lane);
+    }
+}
+
 // ---- the kernel ----------------------------------------------------------------------------
 
 template <class S, int NG>
@@ -328,11 +429,11 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     unsigned char *gbase = smem + d.group_off + gr * d.group_bytes;
     float4 *tile = (float4 *)gbase;
     _Float16 *un = (_Float16 *)(gbase + d.tile_bytes);
-    _Float16 *xt = un;
-    _Float16 *dyt = xt + TrainLayout<S>::xt_rows * kRowStride;
-    _Float16 *dxt = un;                       // scatter: dX0^T [K0][kRowStride]
-    _Float16 *whi = un + S::K0 * kRowStride;  // scatter weights [sample][wcols], hi
-    _Float16 *wlo = whi + kChunk * d.wcols;   // ... lo
+    _Float16 *xs = un;                          // layer inputs, [sample][kFeatStride]
+    _Float16 *dys = xs + kChunk * kFeatStride;  // layer output gradients, [sample][kFeatStride]
+    _Float16 *dxs = un;                         // scatter: dX0 rows [sample][dx_stride(K0)]
+    _Float16 *whi = un + kChunk * dx_stride(S::K0); // scatter weights [sample][wcols], hi
+    _Float16 *wlo = whi + kChunk * d.wcols;     // ... lo
 
     {
         // Weight image (staged through the group regions, which the tile loop overwrites only
@@ -353,10 +454,10 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 #pragma unroll
     for (int j = 0; j < LY::slots; ++j)
         dwacc[j] = (f16v)0.f;
-    float dbacc[L];
+    float dbt[LY::slots]; // bias-gradient partial of the owned tile (a, 0): feature 32a + c
 #pragma unroll
-    for (int l = 0; l < L; ++l)
-        dbacc[l] = 0.f;
+    for (int j = 0; j < LY::slots; ++j)
+        dbt[j] = 0.f;
     const int col = 32 * wave + c; // this lane's sample column in the group's transposes
 
     // Tiles of the region, several per workgroup when there are more tiles than workgroups;
@@ -448,23 +549,23 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 
         // ---- backward, last layer (mlp.h:302-362)
         h8 dyh[HQ];
-        store_transposed<1, true>(dyt, dyo, col, g);
-        store_transposed<HQ, true>(xt, xh[NH - 1], col, g);
+        store_rows<1>(dys, dyo, col, g);
+        store_rows<HQ>(xs, xh[NH - 1], col, g);
         {
             f16v acc[HA];
             layer_backward_dx<1, HA>(frags + S::bwd_off(L - 1) * kWave, dyo, acc, lane);
             relu_backward<HQ, HA>(acc, xh[NH - 1], dyh);
         }
         __syncthreads();
-        dw_phase<S, L - 1>(xt, dyt, dwacc, dbacc[L - 1], wave, lane, t256);
+        dw_rows<S, L - 1>(xs, dys, dwacc, dbt, wave, lane);
         __syncthreads();
 
         // ---- hidden layers L-2 .. 1
-        backward_hidden<S, L - 2>(xt, dyt, frags, xh, dyh, dwacc, dbacc, col, wave, lane, t256);
+        backward_hidden_rows<S, L - 2>(xs, dys, frags, xh, dyh, dwacc, dbt, col, wave, lane);
 
         // ---- first layer: dW with the gathered inputs, dX = latent gradient
-        store_transposed<HQ, true>(dyt, dyh, col, g);
-        store_inputs_transposed<G>(xt, x0, col, g);
+        store_rows<HQ>(dys, dyh, col, g);
+        store_input_rows<G>(xs, x0, col, g);
         h8 dx0[KQ0];
         {
             constexpr int MA = S::t32(S::K0);
@@ -482,16 +583,16 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
             }
         }
         __syncthreads();
-        dw_phase<S, 0>(xt, dyt, dwacc, dbacc[0], wave, lane, t256);
+        dw_rows<S, 0>(xs, dys, dwacc, dbt, wave, lane);
         __syncthreads();
 
         // ---- latent scatter (train.cu:460-509) as an MFMA reduction over the chunk
-        // Part 1: dX0^T; lane group g fills the weight-row entries of grids g, g + 2 for its
-        // sample (own entries cleared first). A footprint not wholly inside the chunk cell
-        // box (not expected: the box covers every corner a chunk position can reach, up to
-        // fp32 rounding) goes straight into the footprint box or global memory, all 16
-        // channels read back from dX0^T.
-        store_transposed<KQ0, true>(dxt, dx0, col, g);
+        // Part 1: dX0 rows; lane group g fills the weight-row entries of grids g, g + 2 for
+        // its sample (own entries cleared first). A footprint not wholly inside the chunk
+        // cell box (not expected: the box covers every corner a chunk position can reach, up
+        // to fp32 rounding) goes straight into the footprint box or global memory, all 16
+        // channels read back from the dX0 row.
+        store_rows<KQ0, dx_stride(S::K0)>(dxs, dx0, col, g);
         {
             _Float16 *rhi = whi + col * d.wcols, *rlo = wlo + col * d.wcols;
 #pragma unroll
@@ -528,7 +629,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                         const int lx = tx - lox, ly = ty - loy;
                         const bool inbox = lx >= 0 && lx < q.fp_w && ly >= 0 && ly < q.fp_h;
                         for (int ch = 0; ch < 16; ++ch) {
-                            const float val = f.w[corner] * (float)dxt[(16 * gi + ch) * kRowStride + col];
+                            const float val = f.w[corner] * (float)dxs[col * dx_stride(S::K0) + 16 * gi + ch];
                             if (inbox)
                                 lds_add(fp + q.fp_off + (ly * q.fp_w + lx) * 16 + ch, val);
                             else
@@ -552,13 +653,12 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                     if ((task & 3) != wave)
                         continue;
                     const int i16 = lane & 15, grp = lane >> 4;
-                    const _Float16 *bp = dxt + (gi * 16 + i16) * kRowStride + 8 * grp;
                     const int acol = q.wcol0 + 16 * t + 4 * (i16 & 3);
                     f4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int kk = 0; kk < kChunk / 32; ++kk) {
                         const int arow = 32 * kk + 8 * grp + (i16 >> 2);
-                        const h8 bv = *(const h8 *)(bp + 32 * kk);
+                        const h8 bv = read_cols8<dx_stride(S::K0)>(dxs, 32 * kk + 8 * grp, 16 * gi, i16);
                         const h4 h0 = lds_read_tr16(whi + arow * d.wcols + acol);
                         const h4 h1 = lds_read_tr16(whi + (arow + 4) * d.wcols + acol);
                         const h4 l0 = lds_read_tr16(wlo + arow * d.wcols + acol);
@@ -620,8 +720,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                 for (int e = 0; e < 16; ++e)
                     xch[(j * 16 + e) * kTrainThreads + t256] = dwacc[j][e];
 #pragma unroll
-            for (int l = 0; l < L; ++l)
-                xch[(LY::slots * 16 + l) * kTrainThreads + t256] = dbacc[l];
+            for (int j = 0; j < LY::slots; ++j)
+                xch[(LY::slots * 16 + j) * kTrainThreads + t256] = dbt[j];
         }
         __syncthreads();
         if (gr == 1)
@@ -632,8 +732,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
             for (int e = 0; e < 16; ++e)
                 dwacc[j][e] += xch[(j * 16 + e) * kTrainThreads + t256];
 #pragma unroll
-        for (int l = 0; l < L; ++l)
-            dbacc[l] += xch[(LY::slots * 16 + l) * kTrainThreads + t256];
+        for (int j = 0; j < LY::slots; ++j)
+            dbt[j] += xch[(LY::slots * 16 + j) * kTrainThreads + t256];
     }
     float *part = d.partial + (int64_t)blockIdx.x * S::grad_total();
 #pragma unroll
@@ -665,15 +765,16 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                     part[off + n * kin + k] = dwacc[j][e];
                 }
             }
+            // Tile (a, 0) carries the bias gradient of rows 32a + c: lane groups 0 and 1
+            // summed disjoint halves of every sample block.
+            const float db = dbt[j] + __shfl_xor(dbt[j], 32);
+            if (bb == 0 && g == 0 && 32 * a + c < kout) {
+                const int row = 32 * a + c;
+                const int n = l == L - 1 ? perm_row(d.perm, row) : row;
+                part[off + kout * kin + n] = db;
+            }
         }
     }
-#pragma unroll
-    for (int l = 0; l < L; ++l)
-        if (t256 < 4 * S::kout(l) && (t256 & 3) == 0) {
-            const int row = t256 >> 2;
-            const int n = l == L - 1 ? perm_row(d.perm, row) : row;
-            part[S::grad_off(l) + S::kout(l) * S::kin(l) + n] = dbacc[l];
-        }
 }
 
 // ---- launchers ---------------------------------------------------------------------------
@@ -739,14 +840,8 @@ size_t train16_raw_bytes(int shape)
 
 size_t train16_transpose_bytes(int shape)
 {
-    switch (shape) {
-    case kShapeC2:
-        return TrainLayout<ShapeC2>::transpose_bytes;
-    case kShapeC4:
-        return TrainLayout<ShapeC4>::transpose_bytes;
-    default:
-        return 0;
-    }
+    // Layer inputs and output gradients as sample rows.
+    return shape == kShapeC2 || shape == kShapeC4 ? 2 * kChunk * kFeatStride * 2 : 0;
 }
 
 hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream_t s)
