@@ -18,7 +18,9 @@ constexpr int kChunkH = 8;
 constexpr int kChunk = kChunkW * kChunkH;
 constexpr int kTrainThreads = 256;
 constexpr int kRowStride = kChunk + 8; // fp16 row stride of the LDS transposes
-constexpr int kFeatStride = 72;         // fp16 row stride of the 16-channel kernel's sample rows
+// fp16 row stride of the 16-channel kernel's sample rows: 34 dwords, so that the 8-byte
+// stores of 16 consecutive rows (what gfx950's LDS serves per cycle) hit distinct banks.
+constexpr int kFeatStride = 68;
 // ... and of its dX0 rows (k0 inputs): 16 halves of padding put the four rows of one
 // transposed read in different LDS banks.
 __host__ __device__ constexpr int dx_stride(int k0) { return k0 + 16; }

@@ -329,13 +329,17 @@ __device__ __forceinline__ void store_rows(_Float16 *buf, const h8 (&v)[NQ], int
     }
 }
 
-// Layer-0 inputs in grid_feature order: eight consecutive features per fragment.
+// Layer-0 inputs in grid_feature order: eight consecutive features per fragment (two
+// 8-byte stores: rows are 8-byte aligned).
 template <int G>
 __device__ __forceinline__ void store_input_rows(_Float16 *buf, const h8 (&v)[G], int col, int g)
 {
 #pragma unroll
-    for (int q = 0; q < G; ++q)
-        *(h8 *)(buf + col * kFeatStride + grid_feature(q, g, 0)) = v[q];
+    for (int q = 0; q < G; ++q) {
+        _Float16 *p = buf + col * kFeatStride + grid_feature(q, g, 0);
+        *(h4 *)p = __builtin_shufflevector(v[q], v[q], 0, 1, 2, 3);
+        *(h4 *)(p + 4) = __builtin_shufflevector(v[q], v[q], 4, 5, 6, 7);
+    }
 }
 
 // Samples s0 .. s0 + 7 of feature f0 + i16 (i16 = lane within its 16-lane group; s0 and f0
