@@ -392,6 +392,10 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             return;
     }
     d.fp_floats = fp;
+    // Rows of an odd number of 16-byte chunks: each lane clears its own row with 16-byte
+    // stores, which then fall in distinct LDS banks.
+    if (wcols % 16 == 0)
+        wcols += 8;
     d.wcols = wcols;
     const size_t head = train16_head_bytes(plan->shape);
     const size_t scatter = ((size_t)kChunk * dx_stride(p->mlp.sizes[0]) + 2 * (size_t)kChunk * wcols) * 2;

@@ -21,9 +21,9 @@ constexpr int kRowStride = kChunk + 8; // fp16 row stride of the LDS transposes
 // fp16 row stride of the 16-channel kernel's sample rows: 34 dwords, so that the 8-byte
 // stores of 16 consecutive rows (what gfx950's LDS serves per cycle) hit distinct banks.
 constexpr int kFeatStride = 68;
-// ... and of its dX0 rows (k0 inputs): 16 halves of padding put the four rows of one
-// transposed read in different LDS banks.
-__host__ __device__ constexpr int dx_stride(int k0) { return k0 + 16; }
+// ... and of its dX0 rows (k0 inputs): k0 + 4 halves (an odd number of 8-byte chunks) puts
+// the 8-byte stores of 16 consecutive rows in distinct LDS banks.
+__host__ __device__ constexpr int dx_stride(int k0) { return k0 + 4; }
 // Catmull-Rom target tile of one chunk: texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of every
 // reference texture, float4 each (covers all 16 taps of every jittered sample of the chunk).
 constexpr int kTileX0 = 3;
