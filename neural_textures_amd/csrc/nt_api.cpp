@@ -401,7 +401,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     const size_t scatter = ((size_t)kChunk * dx_stride(p->mlp.sizes[0]) + 2 * (size_t)kChunk * wcols) * 2;
     size_t un = train16_transpose_bytes(plan->shape);
     un = scatter > un ? scatter : un;
-    d.tile_bytes = d.ntex * kTileW * kTileH * 16;
+    d.tile_bytes = d.ntex * kT16TileSlots * 16;
     d.group_bytes = (int)((d.tile_bytes + un + 15) & ~(size_t)15);
     // The second group's region carries its dW accumulators to the first at the end.
     const size_t handoff = (size_t)train16_slots(plan->shape) * 17 * kTrainThreads * 4;

@@ -29,6 +29,15 @@ __host__ __device__ constexpr int dx_stride(int k0) { return k0 + 4; }
 constexpr int kTileX0 = 3;
 constexpr int kTileW = kChunkW + 7;
 constexpr int kTileH = kChunkH + 7;
+// The 16-channel train kernel's tile: texels [cx0-2, cx0+18) x [cy0-2, cy0+10) of every
+// texture, exactly the Catmull-Rom taps of a chunk's jittered positions (a position in
+// texel x has taps x-2 .. x+2), in rows of 32 float4 slots: rows 256-byte multiples apart,
+// so the 16-byte tap reads of a 16-lane group never share LDS banks across rows.
+constexpr int kT16TileX0 = 2;
+constexpr int kT16TileW = kChunkW + 4;
+constexpr int kT16TileH = kChunkH + 4;
+constexpr int kT16TileStride = 32;
+constexpr int kT16TileSlots = kT16TileH * kT16TileStride;
 
 // One latent grid at the mip levels a kernel samples.
 struct GridDesc {

@@ -27,7 +27,6 @@
 
 namespace ntk {
 
-constexpr int kTileTexels = kTileW * kTileH;
 
 template <class S, int NG>
 struct T16Layout {
@@ -169,27 +168,27 @@ __device__ __forceinline__ h4 lds_read_tr16(const _Float16 *p)
     return __builtin_bit_cast(h4, v);
 }
 
-// Start the copy of the chunk's target tile (texels [cx0-3, cx0+20) x [cy0-3, cy0+12) of
+// Start the copy of the chunk's target tile (texels [cx0-2, cx0+18) x [cy0-2, cy0+10) of
 // every texture, wrapped like the reference's texture objects, main.cpp:613-621) into the
-// group's LDS tile with global_load_lds_dwordx4: wave w copies texels 64(w + 4k) + lane of
-// each texture, each wave instruction filling 64 consecutive float4 slots. No
-// registers are held; the caller waits for vmcnt(0) before the barrier that publishes it.
+// group's LDS tile with global_load_lds_dwordx4: wave w copies slots 64(w + 4k) + lane of
+// each texture, each wave instruction filling 64 consecutive float4 slots (two tile rows;
+// the 12 padding slots of a row repeat its last texel). No registers are held; the caller
+// waits for vmcnt(0) before the barrier that publishes it.
 __device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *tile, int cx0, int cy0,
                                                  int wave, int lane)
 {
-    for (int base = 64 * wave; base < kTileTexels; base += 64 * 4) {
+    static_assert(kT16TileSlots % 64 == 0, "whole wave instructions");
+    for (int base = 64 * wave; base < kT16TileSlots; base += 64 * 4) {
         const int i = base + lane;
-        if (i < kTileTexels) {
-            const int ty = i / kTileW, tx = i - ty * kTileW;
-            int gx = cx0 - kTileX0 + tx, gy = cy0 - kTileX0 + ty;
-            gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
-            gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
-            const int64_t off = ((int64_t)gy * d.image_w + gx) * 4; // same texel of every texture
-            for (int t = 0; t < d.ntex; ++t)
-                __builtin_amdgcn_global_load_lds((const void *)(d.tex[t] + off),
-                                                 (__attribute__((address_space(3))) void *)(tile + t * kTileTexels + base),
-                                                 16, 0, 0);
-        }
+        const int ty = i / kT16TileStride, tx = min(i % kT16TileStride, kT16TileW - 1);
+        int gx = cx0 - kT16TileX0 + tx, gy = cy0 - kT16TileX0 + ty;
+        gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
+        gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
+        const int64_t off = ((int64_t)gy * d.image_w + gx) * 4; // same texel of every texture
+        for (int t = 0; t < d.ntex; ++t)
+            __builtin_amdgcn_global_load_lds((const void *)(d.tex[t] + off),
+                                             (__attribute__((address_space(3))) void *)(tile + t * kT16TileSlots + base),
+                                             16, 0, 0);
     }
 }
 
@@ -203,7 +202,7 @@ __device__ __forceinline__ void cr_taps(const float4 *base, const float (&wx)[4]
     for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 p = base[jj * kTileW + i];
+            const float4 p = base[jj * kT16TileStride + i];
             const float wxy = wx[i] * wy[jj];
             acc[0] = fmaf(p.x, wxy, acc[0]);
             acc[1] = fmaf(p.y, wxy, acc[1]);
@@ -222,15 +221,15 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
 {
     float wx[4], wy[4];
     const int gx0 = cr_axis(u, d.image_w, wx), gy0 = cr_axis(v, d.image_h, wy);
-    const int x0 = gx0 - (cx0 - kTileX0), y0 = gy0 - (cy0 - kTileX0);
-    const bool inside = x0 >= 0 && x0 + 3 < kTileW && y0 >= 0 && y0 + 3 < kTileH;
+    const int x0 = gx0 - (cx0 - kT16TileX0), y0 = gy0 - (cy0 - kT16TileX0);
+    const bool inside = x0 >= 0 && x0 + 3 < kT16TileW && y0 >= 0 && y0 + 3 < kT16TileH;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int ti = g + 2 * j;
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
         if (ti < d.ntex) {
             if (inside) {
-                const float4 *base = tile + ti * kTileTexels + y0 * kTileW + x0;
+                const float4 *base = tile + ti * kT16TileSlots + y0 * kT16TileStride + x0;
                 if (d.four_channels)
                     cr_taps<true>(base, wx, wy, acc);
                 else
