@@ -414,6 +414,15 @@ __device__ __forceinline__ void backward_hidden_rows(_Float16 *xs, _Float16 *dys
     }
 }
 
+// Column of chunk cell `cell` in the scatter weight rows: within each 16-cell tile the two
+// 2-bit halves of the index are swapped, so that D row 4grp + r of the reduction's MFMA
+// (lane group grp, element r) holds cell 16t + 4r + grp, and the four cells one LDS float
+// add of the footprint box covers are consecutive (distinct banks) instead of four apart.
+__device__ __forceinline__ int cell_column(int cell)
+{
+    return (cell & ~15) | ((cell & 3) << 2) | ((cell >> 2) & 3);
+}
+
 // ---- the kernel ----------------------------------------------------------------------------
 
 template <class S, int NG>
@@ -619,7 +628,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                 if (valid && inside) {
 #pragma unroll
                     for (int corner = 0; corner < 4; ++corner) {
-                        const int k = wcol0 + (cy + (corner >> 1)) * cb_w + cx + (corner & 1);
+                        const int k = wcol0 + cell_column((cy + (corner >> 1)) * cb_w + cx + (corner & 1));
                         const _Float16 hi = (_Float16)f.w[corner];
                         rhi[k] = hi;
                         rlo[k] = (_Float16)(f.w[corner] - (float)hi);
@@ -671,7 +680,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int cell = 16 * t + 4 * grp + r;
+                        const int cell = 16 * t + 4 * r + grp; // D row 4grp + r holds column 16t + 4grp + r
                         if (cell >= q.ncell || acc[r] == 0.f)
                             continue;
                         const int cy = (int)(((float)cell + 0.5f) * q.inv_cb_w);
