@@ -137,6 +137,10 @@ TRAIN_CASES = [
     ("c2", 128, (64, 48), (100, 90), abi.NT_UNCONSTRAINED),     # wraps: clamped edge samples
     ("c4", 128, (64, 32), (96, 120), abi.NT_UNCONSTRAINED),
     ("c4", 128, (64, 32), (8, 8), abi.NT_UNCONSTRAINED),
+    # image sizes that are not powers of two: positions divide instead of scaling by an exact
+    # reciprocal, and footprints come from inexact products
+    ("c2", 100, (64, 32), (7, 13), abi.NT_UNCONSTRAINED),
+    ("c4", 96, (64, 32), (30, 50), abi.NT_UNCONSTRAINED),
     ("ref", 64, (32, 16), (0, 0), abi.NT_BLOCK_FEATURES),
     ("ref", 64, (32, 16), (5, 7), abi.NT_FINALIZE),
     ("c2", 64, (32, 16), (3, 9), abi.NT_BLOCK_FEATURES),
