@@ -366,6 +366,13 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             cap = std::min(cap, std::atoi(env));
     d.nwg = std::min(d.ntiles, cap);
     d.xcd_per = (d.ntiles % 8 == 0 && d.nwg % 8 == 0) ? d.ntiles / 8 : 0;
+    // Margins of the footprint box and the chunk cell box beyond the texels positions can
+    // reach. NT_TRAIN_TEST_MARGINS=0 drops them: tests use it to drive the scatter's
+    // out-of-box paths (straight box adds, global atomics), which positions never take.
+    int box_margin = 4, cell_margin = 2;
+    if (const char *env = std::getenv("NT_TRAIN_TEST_MARGINS"))
+        if (env[0] == '0' && env[1] == 0)
+            box_margin = cell_margin = 0;
     int fp = 0, wcols = 0;
     for (int gi = 0; gi < G; ++gi) {
         const nt_grid &g = p->latents.grids[gi];
@@ -375,12 +382,12 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         q.grads = g.grads + g.mip_offset[0] * C;
         q.w = g.width;
         q.h = g.height;
-        q.fp_w = (int)std::ceil(4 * kChunkW * rx) + 4;
-        q.fp_h = (int)std::ceil(kChunkH * NG * ry) + 4;
+        q.fp_w = (int)std::ceil(4 * kChunkW * rx) + box_margin;
+        q.fp_h = (int)std::ceil(kChunkH * NG * ry) + box_margin;
         q.fp_off = fp;
         fp += q.fp_w * q.fp_h * 16;
-        q.cb_w = (int)std::ceil(kChunkW * rx) + 2;
-        q.cb_h = (int)std::ceil(kChunkH * ry) + 2;
+        q.cb_w = (int)std::ceil(kChunkW * rx) + cell_margin;
+        q.cb_h = (int)std::ceil(kChunkH * ry) + cell_margin;
         q.ncell = q.cb_w * q.cb_h;
         q.wcol0 = wcols;
         wcols += 16 * ((q.ncell + 15) / 16);

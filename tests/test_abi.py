@@ -137,13 +137,16 @@ def test_argument_errors_enqueue_nothing(lib):
     assert e.value.status == abi.NT_ERR_NULL_POINTER
 
 
+@pytest.mark.parametrize("margins", [None, "0"])
 @pytest.mark.parametrize("shape,ng", [("c2", 2), ("c4", 1)])
-def test_config_shapes_plan_the_16_channel_kernel(lib, shape, ng):
+def test_config_shapes_plan_the_16_channel_kernel(lib, shape, ng, margins, monkeypatch):
     """The BASELINE config 2 / 4 shapes (grid-to-image ratios, textures, MLP) must be planned
     on the 16-channel train kernel: its LDS layout has to fit. That plan's workspace is
     exactly one gradient partial row per 64 x 8*groups tile (no prepared weight image), which
     tells it apart from the generic kernel's."""
     from helpers import make_state
+    if margins is not None:  # the out-of-box scatter test runs the same kernel
+        monkeypatch.setenv("NT_TRAIN_TEST_MARGINS", margins)
     st = make_state(shape, image=256, region=(64, 64))
     p = st.params()
     sizes = list(st.net.sizes)

@@ -196,6 +196,21 @@ def test_train_step_several_tiles_per_workgroup(lib, O, shape, monkeypatch):
         assert np.all(to_np(gg.grads)[g.grads == 0] == 0)
 
 
+@pytest.mark.parametrize("shape", ["c2", "c4"])
+def test_train_step_scatter_out_of_box_paths(lib, O, shape, monkeypatch):
+    """Without the margins of the chunk cell box and the footprint box, many footprints fall
+    outside them: the scatter adds those straight into the box or, outside the box, with
+    global atomics. Gradients still match the oracle's."""
+    say(f"case: train {shape} without box margins")
+    monkeypatch.setenv("NT_TRAIN_TEST_MARGINS", "0")
+    st, gs = run_train_pair(lib, O, shape, 128, (64, 32), (11, 21), abi.NT_UNCONSTRAINED)
+    for l in range(st.net.num_layers):
+        assert rel_err(to_np(gs.net.weight_grads[l]), st.net.weight_grads[l]) <= MLP_TOL, f"dW{l}"
+    for gi, (g, gg) in enumerate(zip(st.grids, gs.grids)):
+        assert rel_err(to_np(gg.grads), g.grads) <= MLP_TOL, f"latent grad {gi}"
+        assert np.all(to_np(gg.grads)[g.grads == 0] == 0)
+
+
 @pytest.mark.parametrize("shape", ["ref", "c2", "c4"])
 def test_train_step_random_texels(lib, O, shape):
     """NT_SAMPLES_RANDOM: samples anywhere in the image (no footprint box or target tile);
