@@ -366,14 +366,14 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             cap = std::min(cap, std::atoi(env));
     d.nwg = std::min(d.ntiles, cap);
     d.xcd_per = (d.ntiles % 8 == 0 && d.nwg % 8 == 0) ? d.ntiles / 8 : 0;
-    // Margins of the footprint box and the chunk cell box beyond the texels positions can
-    // reach. NT_TRAIN_TEST_MARGINS=0 drops them: tests use it to drive the scatter's
-    // out-of-box paths (straight box adds, global atomics), which positions never take.
-    int box_margin = 4, cell_margin = 2;
+    // Margin of the chunk cell box beyond the cells positions can reach.
+    // NT_TRAIN_TEST_MARGINS=0 drops it: tests use it to drive the scatter's out-of-box path
+    // (per-sample global atomics), which positions never take.
+    int cell_margin = 2;
     if (const char *env = std::getenv("NT_TRAIN_TEST_MARGINS"))
         if (env[0] == '0' && env[1] == 0)
-            box_margin = cell_margin = 0;
-    int fp = 0, wcols = 0;
+            cell_margin = 0;
+    int wcols = 0;
     for (int gi = 0; gi < G; ++gi) {
         const nt_grid &g = p->latents.grids[gi];
         Grid16 &q = d.grid[gi];
@@ -382,23 +382,17 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         q.grads = g.grads + g.mip_offset[0] * C;
         q.w = g.width;
         q.h = g.height;
-        q.fp_w = (int)std::ceil(4 * kChunkW * rx) + box_margin;
-        q.fp_h = (int)std::ceil(kChunkH * NG * ry) + box_margin;
-        q.fp_off = fp;
-        fp += q.fp_w * q.fp_h * 16;
         q.cb_w = (int)std::ceil(kChunkW * rx) + cell_margin;
         q.cb_h = (int)std::ceil(kChunkH * ry) + cell_margin;
         q.ncell = q.cb_w * q.cb_h;
         q.wcol0 = wcols;
         wcols += 16 * ((q.ncell + 15) / 16);
         q.inv_cb_w = 1.f / (float)q.cb_w;
-        q.inv_fp_w = 1.f / (float)q.fp_w;
         q.rx = (float)g.width / (float)p->image_width;
         q.ry = (float)g.height / (float)p->image_height;
         if (!aligned16(q.values) || !aligned16(q.grads))
             return;
     }
-    d.fp_floats = fp;
     // Rows of an odd number of 16-byte chunks: each lane clears its own row with 16-byte
     // stores, which then fall in distinct LDS banks.
     if (wcols % 16 == 0)
@@ -414,7 +408,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     const size_t handoff = (size_t)train16_slots(plan->shape) * 17 * kTrainThreads * 4;
     if (NG == 2 && (size_t)d.group_bytes < handoff)
         return;
-    d.group_off = (int)((head + (size_t)fp * 4 + 15) & ~(size_t)15);
+    d.group_off = (int)((head + 15) & ~(size_t)15);
     const size_t lds = (size_t)d.group_off + (size_t)NG * d.group_bytes;
     // The prologue stages the fp16 weight matrices in the group regions.
     if (lds > kMaxLds || train16_raw_bytes(plan->shape) > (size_t)NG * d.group_bytes)

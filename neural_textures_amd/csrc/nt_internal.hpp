@@ -91,10 +91,9 @@ struct Grid16 {
     const float *values; // mip 0, [texel][16]
     float *grads;
     int w, h;
-    int fp_w, fp_h, fp_off; // workgroup footprint box in LDS: [fp_h][fp_w][16] floats at fp_off
     int cb_w, cb_h, ncell;  // chunk cell box (cb_w x cb_h cells)
     int wcol0;              // first column of this grid's cells in the scatter weight rows
-    float inv_cb_w, inv_fp_w;
+    float inv_cb_w;
     float rx, ry; // grid texels per image texel
 };
 
@@ -111,7 +110,6 @@ struct Train16Desc {
     // reciprocal then equals the quotient exactly), else 0 (divide).
     float inv_w, inv_h, inv_samples;
     int tiles_x, ntiles, nwg, xcd_per; // xcd_per > 0: workgroups of one XCD take consecutive tiles
-    int fp_floats;
     int group_off, group_bytes, tile_bytes; // per 4-wave group: target tile, then the union
     int wcols;                              // halves per scatter-weight row (one row per sample)
     uint64_t perm;                          // nibble r: output index of output row r

@@ -6,21 +6,26 @@
 // SIMD, so one wave's LDS and memory latency hides behind the other's work). It owns a
 // 64 x 8NG block of region positions; group gr walks rows [8gr, 8gr + 8) as four 16 x 8
 // chunks of 128 samples, one 32-sample MFMA tile per wave. Per chunk:
-//   - the group's Catmull-Rom target tile is fetched into registers first and written to
-//     its own LDS region after the forward pass, so the loads overlap sampling and MLP;
+//   - the group's Catmull-Rom target tile is copied into its LDS region by DMA
+//     (global_load_lds) at the chunk start and published after the forward pass, so the
+//     loads overlap sampling and MLP;
 //   - lane group g (lane = 32g + c, sample c) gathers grids g and g + 2 only, so each
 //     lane computes one bilinear footprint per fragment pair; the layer-0 weight
 //     fragments carry the matching input-feature order;
 //   - output rows are ordered 4t + channel for reference texture t, so lane group g
 //     evaluates exactly textures g and g + 2 (16 exact Catmull-Rom taps from LDS); the
 //     last layer's weight fragments carry the matching output permutation;
-//   - dW = X^T dY per layer on MFMA over the group's 128 samples from LDS transposes,
-//     each wave owning fixed 32x32 dW tiles accumulated in fp32 registers;
+//   - dW = X^T dY per layer on MFMA over the group's 128 samples: sample rows in LDS read
+//     back transposed (ds_read_b64_tr_b16), each wave owning fixed 32x32 dW tiles
+//     accumulated in fp32 registers;
 //   - the latent scatter is an MFMA reduction D[cell][ch] = sum_s W[cell][s] dX0[s][ch]
 //     over the chunk's cell box (fp32 corner weights split into fp16 hi + lo). Each lane
 //     keeps one scatter-weight row per sample and clears only its own entries, and the
-//     rows are read transposed with ds_read_b64_tr_b16. D is added into the workgroup's
-//     footprint box with LDS float adds and flushed once with global float atomics.
+//     rows are read transposed with ds_read_b64_tr_b16. D goes to the latent gradients
+//     with global float atomics, each instruction adding four whole 64-byte texel records
+//     (an LDS footprint box with ds_add_f32 in between cost more: an LDS float atomic
+//     occupies the LDS for 192 cycles per wave instruction on gfx950, and the chunks'
+//     cell boxes overlap too little for the box to save global traffic).
 // MLP gradients go to one partial row per group, summed by the deterministic two-stage
 // reduction of nt_train.hip.
 #include "nt_train_parts.hpp"
@@ -416,8 +421,8 @@ __device__ __forceinline__ void backward_hidden_rows(_Float16 *xs, _Float16 *dys
 
 // Column of chunk cell `cell` in the scatter weight rows: within each 16-cell tile the two
 // 2-bit halves of the index are swapped, so that D row 4grp + r of the reduction's MFMA
-// (lane group grp, element r) holds cell 16t + 4r + grp, and the four cells one LDS float
-// add of the footprint box covers are consecutive (distinct banks) instead of four apart.
+// (lane group grp, element r) holds cell 16t + 4r + grp, and the four cells one atomic
+// instruction covers are consecutive (neighbouring texel records) instead of four apart.
 __device__ __forceinline__ int cell_column(int cell)
 {
     return (cell & ~15) | ((cell & 3) << 2) | ((cell >> 2) & 3);
@@ -434,7 +439,6 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     extern __shared__ __align__(16) unsigned char smem[];
     h8 *frags = (h8 *)smem;
     float *bias = (float *)(smem + LY::frag_bytes);
-    float *fp = (float *)(smem + LY::head_bytes);
 
     const int tid = threadIdx.x, t256 = tid & (kTrainThreads - 1), gr = tid >> 8;
     const int lane = tid & 63, wave = t256 >> 6, c = lane & 31, g = lane >> 5;
@@ -449,13 +453,10 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 
     {
         // Weight image (staged through the group regions, which the tile loop overwrites only
-        // after the barriers below), biases, and the cleared footprint box.
+        // after the barriers below) and biases.
         constexpr int NT = kTrainThreads * NG;
         uint16_t *raw = (uint16_t *)(smem + d.group_off);
         stage_weights16<S, NT>(d, raw, bias, tid);
-        float4 *f4 = (float4 *)fp;
-        for (int i = tid; i < d.fp_floats / 4; i += NT)
-            f4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         __syncthreads();
         for (int f = __builtin_amdgcn_readfirstlane(tid >> 6); f < S::all_frags(); f += NT / kWave)
             frags[f * kWave + lane] = weight_fragment16<S>(raw, d.perm, f, lane);
@@ -473,20 +474,12 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     const int col = 32 * wave + c; // this lane's sample column in the group's transposes
 
     // Tiles of the region, several per workgroup when there are more tiles than workgroups;
-    // the MLP gradient accumulates over all of them, the footprint box is flushed per tile.
+    // the MLP gradient accumulates over all of them.
     for (int b0 = blockIdx.x; b0 < d.ntiles; b0 += gridDim.x) {
     int b = b0;
     if (d.xcd_per > 0)
         b = (b & 7) * d.xcd_per + (b >> 3); // the workgroups of one XCD share an L2: give them neighbouring tiles
     const int tx0 = (b % d.tiles_x) * (kChunkW * 4), ty0 = (b / d.tiles_x) * (kChunkH * NG);
-    // Footprint box origin per grid: the lowest texel any sample of the tile can touch.
-    int flo_x[G], flo_y[G];
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        const Grid16 &q = d.grid[gi];
-        flo_x[gi] = (int)floorf((float)(d.off_x + tx0) * (float)q.w / (float)d.image_w - 0.5f) - 1;
-        flo_y[gi] = (int)floorf((float)(d.off_y + ty0) * (float)q.h / (float)d.image_h - 0.5f) - 1;
-    }
 
     for (int chunk = 0; chunk < 4; ++chunk) {
         const int cx0 = d.off_x + tx0 + chunk * kChunkW, cy0 = d.off_y + ty0 + kChunkH * gr;
@@ -602,8 +595,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         // Part 1: dX0 rows; lane group g fills the weight-row entries of grids g, g + 2 for
         // its sample (own entries cleared first). A footprint not wholly inside the chunk
         // cell box (not expected: the box covers every corner a chunk position can reach, up
-        // to fp32 rounding) goes straight into the footprint box or global memory, all 16
-        // channels read back from the dX0 row.
+        // to fp32 rounding) goes straight to global memory, all 16 channels read back from
+        // the dX0 row.
         store_rows<KQ0, dx_stride(S::K0)>(dxs, dx0, col, g);
         {
             _Float16 *rhi = whi + col * d.wcols, *rlo = wlo + col * d.wcols;
@@ -635,17 +628,11 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                     }
                 } else if (valid) {
                     const Grid16 &q = g ? qb : qa;
-                    const int lox = g ? flo_x[2 * j + 1] : flo_x[2 * j], loy = g ? flo_y[2 * j + 1] : flo_y[2 * j];
                     for (int corner = 0; corner < 4; ++corner) {
-                        const int tx = f.x0 + (corner & 1), ty = f.y0 + (corner >> 1);
-                        const int lx = tx - lox, ly = ty - loy;
-                        const bool inbox = lx >= 0 && lx < q.fp_w && ly >= 0 && ly < q.fp_h;
+                        const int tx = wrap_near(f.x0 + (corner & 1), q.w), ty = wrap_near(f.y0 + (corner >> 1), q.h);
                         for (int ch = 0; ch < 16; ++ch) {
                             const float val = f.w[corner] * (float)dxs[col * dx_stride(S::K0) + 16 * gi + ch];
-                            if (inbox)
-                                lds_add(fp + q.fp_off + (ly * q.fp_w + lx) * 16 + ch, val);
-                            else
-                                global_add(q.grads + ((int64_t)wrap_near(ty, q.h) * q.w + wrap_near(tx, q.w)) * 16 + ch, val);
+                            global_add(q.grads + ((int64_t)ty * q.w + tx) * 16 + ch, val);
                         }
                     }
                 }
@@ -685,12 +672,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                             continue;
                         const int cy = (int)(((float)cell + 0.5f) * q.inv_cb_w);
                         const int cxx = cell - cy * q.cb_w;
-                        const int tx = bx + cxx, ty = by + cy;
-                        const int lx = tx - flo_x[gi], ly = ty - flo_y[gi];
-                        if (lx >= 0 && lx < q.fp_w && ly >= 0 && ly < q.fp_h)
-                            lds_add(fp + q.fp_off + (ly * q.fp_w + lx) * 16 + i16, acc[r]);
-                        else
-                            global_add(q.grads + ((int64_t)wrap_near(ty, q.h) * q.w + wrap_near(tx, q.w)) * 16 + i16, acc[r]);
+                        const int tx = wrap_near(bx + cxx, q.w), ty = wrap_near(by + cy, q.h);
+                        global_add(q.grads + ((int64_t)ty * q.w + tx) * 16 + i16, acc[r]);
                     }
                 }
             }
@@ -698,28 +681,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         // The next chunk writes the union only after its first barrier.
     }
 
-    __syncthreads();
-    // ---- flush the footprint box with global float atomics, clearing it for the next tile
-    // (the next tile's first box access follows at least one barrier). Lane i takes float i,
-    // so one atomic instruction covers 64 consecutive floats (four texels) of the gradient
-    // array: four full 64-byte lines per instruction.
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        const Grid16 &q = d.grid[gi];
-        float *box = fp + q.fp_off;
-        const int n = q.fp_w * q.fp_h * 16;
-        for (int i = tid; i < n; i += kTrainThreads * NG) {
-            const float val = box[i];
-            if (val == 0.f)
-                continue;
-            box[i] = 0.f;
-            const int cell = i >> 4, ch = i & 15;
-            const int ly = (int)(((float)cell + 0.5f) * q.inv_fp_w), lx = cell - ly * q.fp_w;
-            const int gx = wrap_near(flo_x[gi] + lx, q.w), gy = wrap_near(flo_y[gi] + ly, q.h);
-            global_add(q.grads + ((int64_t)gy * q.w + gx) * 16 + ch, val);
-        }
-    }
     } // tiles
+    __syncthreads(); // group 1's last scatter reads are done before its region is reused below
 
     // ---- the workgroup's MLP gradient partial (output rows of the last layer un-permuted):
     // group 1 hands its accumulators to group 0 through its own (now idle) LDS region.

@@ -198,9 +198,8 @@ def test_train_step_several_tiles_per_workgroup(lib, O, shape, monkeypatch):
 
 @pytest.mark.parametrize("shape", ["c2", "c4"])
 def test_train_step_scatter_out_of_box_paths(lib, O, shape, monkeypatch):
-    """Without the margins of the chunk cell box and the footprint box, many footprints fall
-    outside them: the scatter adds those straight into the box or, outside the box, with
-    global atomics. Gradients still match the oracle's."""
+    """Without the margin of the chunk cell box, many footprints fall outside it: the
+    scatter adds those per sample with global atomics. Gradients still match the oracle's."""
     say(f"case: train {shape} without box margins")
     monkeypatch.setenv("NT_TRAIN_TEST_MARGINS", "0")
     st, gs = run_train_pair(lib, O, shape, 128, (64, 32), (11, 21), abi.NT_UNCONSTRAINED)
