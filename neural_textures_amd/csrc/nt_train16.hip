@@ -39,7 +39,28 @@ struct T16Layout {
     static constexpr int frag_bytes = S::all_frags() * kWave * 16;
     static constexpr int bias_bytes = ((S::bias_total() * 4 + 15) / 16) * 16;
     static constexpr int head_bytes = frag_bytes + bias_bytes;
-    static constexpr int slots = (S::dw_total() + 3) / 4;
+    // dW work items: a layer with at most two 32x32 tiles has each tile's 128-sample
+    // reduction split into two halves (two items), so that all four waves of a group work
+    // in every dW phase. Items are enumerated from the last layer down; wave w owns items
+    // w, w + 4, ... (one accumulator slot each).
+    static constexpr bool split(int l) { return S::dw_tiles(l) <= 2; }
+    static constexpr int items(int l) { return S::dw_tiles(l) * (split(l) ? 2 : 1); }
+    static constexpr int item_start(int l)
+    {
+        int o = 0;
+        for (int j = S::L - 1; j > l; --j)
+            o += items(j);
+        return o;
+    }
+    // Index of layer l's first tile among the split tiles (the end-of-kernel merge buffer).
+    static constexpr int split_start(int l)
+    {
+        int o = 0;
+        for (int j = S::L - 1; j > l; --j)
+            o += split(j) ? S::dw_tiles(j) : 0;
+        return o;
+    }
+    static constexpr int slots = (item_start(-1) + 3) / 4;
 };
 
 // ---- weight preparation (the workgroup prologue) ----------------------------------------
@@ -364,19 +385,24 @@ template <class S, int l>
 __device__ __forceinline__ void dw_rows(const _Float16 *xs, const _Float16 *dys, f16v (&acc)[T16Layout<S, 1>::slots],
                                         float (&db)[T16Layout<S, 1>::slots], int wave, int lane)
 {
+    using LY = T16Layout<S, 1>;
     constexpr int kin = S::kin(l), kout = S::kout(l);
-    constexpr int KB = S::t32(kin), NA = S::t32(kout);
-    constexpr int start = S::dw_start(l), ntiles = NA * KB;
+    constexpr int KB = S::t32(kin);
+    constexpr bool SPLIT = LY::split(l);
+    constexpr int start = LY::item_start(l), nitems = LY::items(l);
+    constexpr int QN = SPLIT ? kChunk / 32 : kChunk / 16; // 16-sample k-steps per item
     const int c = lane & 31, g = lane >> 5, i16 = lane & 15, half = 16 * (c >> 4);
     const h2 one = {(_Float16)1.f, (_Float16)1.f};
 #pragma unroll
-    for (int j = 0; j < T16Layout<S, 1>::slots; ++j) {
-        const int t = 4 * j + wave - start;
-        if (t >= 0 && t < ntiles) {
+    for (int j = 0; j < LY::slots; ++j) {
+        const int it = 4 * j + wave - start;
+        if (it >= 0 && it < nitems) {
+            const int t = SPLIT ? it >> 1 : it, q0 = SPLIT ? (it & 1) * QN : 0;
             const int a = t / KB, b = t % KB;
             const bool arow = 32 * a + c < kout, brow = 32 * b + c < kin;
 #pragma unroll
-            for (int q = 0; q < kChunk / 16; ++q) {
+            for (int qq = 0; qq < QN; ++qq) {
+                const int q = q0 + qq;
                 h8 A = read_cols8(dys, 16 * q + 8 * g, 32 * a + half, i16);
                 h8 B = read_cols8(xs, 16 * q + 8 * g, 32 * b + half, i16);
                 if (!arow)
@@ -685,7 +711,9 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     __syncthreads(); // group 1's last scatter reads are done before its region is reused below
 
     // ---- the workgroup's MLP gradient partial (output rows of the last layer un-permuted):
-    // group 1 hands its accumulators to group 0 through its own (now idle) LDS region.
+    // group 1 hands its accumulators to group 0 through its own (now idle) LDS region, then
+    // the owner of the second half of a split dW tile hands it to the owner of the first
+    // half through group 0's region. Every wave takes part in every barrier.
     if constexpr (NG == 2) {
         float *xch = (float *)(smem + d.group_off + d.group_bytes);
         if (gr == 1) {
@@ -699,54 +727,72 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                 xch[(LY::slots * 16 + j) * kTrainThreads + t256] = dbt[j];
         }
         __syncthreads();
-        if (gr == 1)
-            return;
+        if (gr == 0) {
 #pragma unroll
-        for (int j = 0; j < LY::slots; ++j)
+            for (int j = 0; j < LY::slots; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                dwacc[j][e] += xch[(j * 16 + e) * kTrainThreads + t256];
+                for (int e = 0; e < 16; ++e)
+                    dwacc[j][e] += xch[(j * 16 + e) * kTrainThreads + t256];
 #pragma unroll
-        for (int j = 0; j < LY::slots; ++j)
-            dbt[j] += xch[(LY::slots * 16 + j) * kTrainThreads + t256];
+            for (int j = 0; j < LY::slots; ++j)
+                dbt[j] += xch[(LY::slots * 16 + j) * kTrainThreads + t256];
+        }
     }
+    float *xfer = (float *)(smem + d.group_off); // [split tile][17][64 lanes]
     float *part = d.partial + (int64_t)blockIdx.x * S::grad_total();
 #pragma unroll
-    for (int j = 0; j < LY::slots; ++j) {
-        const int t = 4 * j + wave;
-        if (t < S::dw_total()) {
-            int l = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1)
+            __syncthreads();
 #pragma unroll
-            for (int k = 0; k < L; ++k)
-                if (t >= S::dw_start(k) && t < S::dw_start(k) + S::dw_tiles(k))
-                    l = k;
-            int kin = S::kin(0), kout = S::kout(0), start = S::dw_start(0), off = S::grad_off(0);
+        for (int j = 0; j < LY::slots; ++j) {
 #pragma unroll
-            for (int k = 1; k < L; ++k)
-                if (l == k) {
-                    kin = S::kin(k);
-                    kout = S::kout(k);
-                    start = S::dw_start(k);
-                    off = S::grad_off(k);
+            for (int l = 0; l < L; ++l) {
+                const int it = 4 * j + wave - LY::item_start(l);
+                if (gr != 0 || it < 0 || it >= LY::items(l))
+                    continue;
+                const bool split = LY::split(l);
+                const int t = split ? it >> 1 : it;
+                float *x = xfer + (LY::split_start(l) + t) * 17 * kWave + lane;
+                if (pass == 0) {
+                    // second halves of split tiles: to the merge buffer
+                    if (split && (it & 1)) {
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            x[e * kWave] = dwacc[j][e];
+                        x[16 * kWave] = dbt[j];
+                    }
+                    continue;
                 }
-            const int kb = (kin + 31) / 32;
-            const int a = (t - start) / kb, bb = (t - start) % kb;
+                if (split && (it & 1))
+                    continue;
+                f16v acc = dwacc[j];
+                float dbj = dbt[j];
+                if (split) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = 32 * a + 8 * (e >> 2) + 4 * g + (e & 3);
-                const int k = 32 * bb + c;
-                if (row < kout && k < kin) {
+                    for (int e = 0; e < 16; ++e)
+                        acc[e] += x[e * kWave];
+                    dbj += x[16 * kWave];
+                }
+                const int kin = S::kin(l), kout = S::kout(l), off = S::grad_off(l), kb = S::t32(S::kin(l));
+                const int a = t / kb, bb = t % kb;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = 32 * a + 8 * (e >> 2) + 4 * g + (e & 3);
+                    const int k = 32 * bb + c;
+                    if (row < kout && k < kin) {
+                        const int n = l == L - 1 ? perm_row(d.perm, row) : row;
+                        part[off + n * kin + k] = acc[e];
+                    }
+                }
+                // Tile (a, 0) carries the bias gradient of rows 32a + c: lane groups 0 and 1
+                // summed disjoint halves of every sample block.
+                const float db = dbj + __shfl_xor(dbj, 32);
+                if (bb == 0 && g == 0 && 32 * a + c < kout) {
+                    const int row = 32 * a + c;
                     const int n = l == L - 1 ? perm_row(d.perm, row) : row;
-                    part[off + n * kin + k] = dwacc[j][e];
+                    part[off + kout * kin + n] = db;
                 }
-            }
-            // Tile (a, 0) carries the bias gradient of rows 32a + c: lane groups 0 and 1
-            // summed disjoint halves of every sample block.
-            const float db = dbt[j] + __shfl_xor(dbt[j], 32);
-            if (bb == 0 && g == 0 && 32 * a + c < kout) {
-                const int row = 32 * a + c;
-                const int n = l == L - 1 ? perm_row(d.perm, row) : row;
-                part[off + kout * kin + n] = db;
             }
         }
     }
