@@ -912,6 +912,8 @@ int nt_inference(const nt_params *p, void *stream)
     d.count = p->image_width * p->image_height;
     d.image_w = p->image_width;
     d.image_h = p->image_height;
+    d.inv_w = pow2_reciprocal(d.image_w);
+    d.inv_h = pow2_reciprocal(d.image_h);
     d.out32 = p->inference_output;
     d.sse = p->inference_mse_accum;
     d.out_stride = p->mlp.sizes[p->mlp.num_layers];
@@ -1110,6 +1112,8 @@ static bool plan_decode_box(const nt_decode_params *p, const FwdDesc &fd, int sh
     b->G = p->num_grids;
     b->image_w = p->out_width;
     b->image_h = p->out_height;
+    b->inv_w = pow2_reciprocal(b->image_w);
+    b->inv_h = pow2_reciprocal(b->image_h);
     b->blocks_x = (p->out_width + kBoxBlockW - 1) / kBoxBlockW;
     b->blocks_y = (p->out_height + kBoxBlockH - 1) / kBoxBlockH;
     b->out16 = p->output;
@@ -1220,6 +1224,8 @@ int nt_decode(const nt_decode_params *p, void *stream)
     d.count = p->out_width * p->out_height;
     d.image_w = p->out_width;
     d.image_h = p->out_height;
+    d.inv_w = pow2_reciprocal(d.image_w);
+    d.inv_h = pow2_reciprocal(d.image_h);
     d.out16 = p->output;
     d.out_stride = p->mlp.used_outputs;
     d.seed = p->seed;

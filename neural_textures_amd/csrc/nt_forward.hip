@@ -324,8 +324,8 @@ __global__ __launch_bounds__(kFwdThreads, fwd_min_blocks<MODE>()) void forward_k
         } else if constexpr (MODE == kFwdInference) {
             const int sc = valid ? s : 0;
             const int px = sc % d.image_w, py = sc / d.image_w;
-            u = ((float)px + 0.5f) / (float)d.image_w; // train.cu:926-933
-            v = ((float)py + 0.5f) / (float)d.image_h;
+            u = div_pow2((float)px + 0.5f, (float)d.image_w, d.inv_w); // train.cu:926-933
+            v = div_pow2((float)py + 0.5f, (float)d.image_h, d.inv_h);
             sample_bilinear<C, KQ0>(d, u, v, 0.f, g, x0);
         } else { // kFwdDecode, kFwdDecode16
             const int sc = valid ? s : 0;
@@ -336,8 +336,8 @@ __global__ __launch_bounds__(kFwdThreads, fwd_min_blocks<MODE>()) void forward_k
             const float zu = uniform01(st);
             const float posx = clampf(fmaf(d.jitter, jx, (float)px + 0.5f), 0.5f, (float)d.image_w - 0.5f);
             const float posy = clampf(fmaf(d.jitter, jy, (float)py + 0.5f), 0.5f, (float)d.image_h - 0.5f);
-            u = posx / (float)d.image_w;
-            v = posy / (float)d.image_h;
+            u = div_pow2(posx, (float)d.image_w, d.inv_w);
+            v = div_pow2(posy, (float)d.image_h, d.inv_h);
             const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
             if constexpr (kDecode16)
                 sample_decode16<KQ0, MODE == kFwdDecode16>(d, mip_tab, u, v, z, g, x0);
@@ -609,8 +609,8 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
             const float zu = uniform01(st);
             const float posx = clampf(fmaf(d.jitter, jx, (float)cx + 0.5f), 0.5f, (float)d.image_w - 0.5f);
             const float posy = clampf(fmaf(d.jitter, jy, (float)cy + 0.5f), 0.5f, (float)d.image_h - 0.5f);
-            const float u = posx / (float)d.image_w;
-            const float v = posy / (float)d.image_h;
+            const float u = div_pow2(posx, (float)d.image_w, d.inv_w);
+            const float v = div_pow2(posy, (float)d.image_h, d.inv_h);
             const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
             h8 x0[KQ0];
             sample_box16<KQ0>(gtab, tab, box, u, v, z, g, x0);

@@ -187,6 +187,7 @@ struct DecodeBoxDesc {
     BoxGrid grid[NT_MAX_GRIDS];
     int G;
     int image_w, image_h, blocks_x, blocks_y;
+    float inv_w, inv_h; // 1/image_w, 1/image_h when powers of two (exact), else 0 (divide)
     int box_texels;  // all boxes, 32 bytes each
     int lds_box_off; // byte offset of the boxes in dynamic LDS
     uint16_t *out16;
@@ -217,6 +218,7 @@ struct FwdDesc {
     int G, C, ntex;
     int count; // samples (pixels)
     int image_w, image_h;
+    float inv_w, inv_h; // 1/image_w, 1/image_h when powers of two (exact), else 0 (divide)
     const uint16_t *half_values[NT_MAX_GRIDS]; // kFwdDecode16: expanded fp16 texel chains
     const uint16_t *inputs; // kFwdMlp
     const float *uvz;       // kFwdBilinear / kFwdCatmullRom
