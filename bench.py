@@ -38,7 +38,7 @@ FLOP_PER_TRAIN_SAMPLE_C4 = 78336   # 3 x 2 x (64*64*3 + 64*12)
 # HBM bytes per config-2 train-kernel launch: rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000,
 # the factors being what the two counters read for a 256 MiB device copy (--copy-probe).
 # Counters cannot be read live; re-measure whenever the train kernel changes.
-TRAIN_HBM_BYTES_PER_LAUNCH = (7688.2 * 2.0 + 9532.0) * 1024
+TRAIN_HBM_BYTES_PER_LAUNCH = (7640.7 * 2.0 + 11408.1) * 1024
 
 
 def log(msg):

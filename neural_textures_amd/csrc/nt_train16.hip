@@ -211,10 +211,13 @@ __device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *t
         gx = (unsigned)gx < (unsigned)d.image_w ? gx : wrap_coord(gx, d.image_w);
         gy = (unsigned)gy < (unsigned)d.image_h ? gy : wrap_coord(gy, d.image_h);
         const int64_t off = ((int64_t)gy * d.image_w + gx) * 4; // same texel of every texture
-        for (int t = 0; t < d.ntex; ++t)
-            __builtin_amdgcn_global_load_lds((const void *)(d.tex[t] + off),
-                                             (__attribute__((address_space(3))) void *)(tile + t * kT16TileSlots + base),
-                                             16, 0, 0);
+        // Unrolled over the (at most four) textures so that their pointers stay in SGPRs.
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            if (t < d.ntex)
+                __builtin_amdgcn_global_load_lds((const void *)(d.tex[t] + off),
+                                                 (__attribute__((address_space(3))) void *)(tile + t * kT16TileSlots + base),
+                                                 16, 0, 0);
     }
 }
 
