@@ -530,7 +530,7 @@ __device__ __forceinline__ void sample_box16(const int4 *gtab, const int4 *tab, 
             fma_corner16(lo, hi, f.w[1], __builtin_bit_cast(h8, t[2]), __builtin_bit_cast(h8, t[3]));
             fma_corner16(lo, hi, f.w[2], __builtin_bit_cast(h8, t[row]), __builtin_bit_cast(h8, t[row + 1]));
             fma_corner16(lo, hi, f.w[3], __builtin_bit_cast(h8, t[row + 2]), __builtin_bit_cast(h8, t[row + 3]));
-            // One mip level's reads at a time keeps the wave within 128 VGPRs.
+            // One mip level's reads at a time keeps the register peak down.
             __builtin_amdgcn_sched_barrier(0);
         }
         x[2 * j] = lo;
@@ -539,7 +539,7 @@ __device__ __forceinline__ void sample_box16(const int4 *gtab, const int4 *tab, 
 }
 
 template <class S>
-__global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDesc d)
+__global__ __launch_bounds__(kFwdThreads, 3) void decode_box_kernel(DecodeBoxDesc d)
 {
     using LY = FwdLayout<S>;
     constexpr int L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
@@ -597,55 +597,71 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
         }
         __syncthreads();
 
-        for (int t = wave; t < kTiles; t += kFwdWaves) {
-            const int px = bx0 + 32 * (t % (kBoxBlockW / 32)) + c, py = by0 + t / (kBoxBlockW / 32);
-            const bool valid = px < d.image_w && py < d.image_h;
-            const int cx = min(px, d.image_w - 1), cy = min(py, d.image_h - 1);
-            const int s = cy * d.image_w + cx;
-            // Position and mip as forward_kernel<..., Decode16> (pixel index s).
-            uint32_t st = mix_seed((uint32_t)s, d.seed);
-            const float jx = uniform01(st) - 0.5f;
-            const float jy = uniform01(st) - 0.5f;
-            const float zu = uniform01(st);
-            const float posx = clampf(fmaf(d.jitter, jx, (float)cx + 0.5f), 0.5f, (float)d.image_w - 0.5f);
-            const float posy = clampf(fmaf(d.jitter, jy, (float)cy + 0.5f), 0.5f, (float)d.image_h - 0.5f);
-            const float u = div_pow2(posx, (float)d.image_w, d.inv_w);
-            const float v = div_pow2(posy, (float)d.image_h, d.inv_h);
-            const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
-            h8 x0[KQ0];
-            sample_box16<KQ0>(gtab, tab, box, u, v, z, g, x0);
+        // Two tiles per wave at a time (t and t + kFwdWaves), sharing the weight reads.
+        static_assert(kTiles % (2 * kFwdWaves) == 0, "whole tile pairs per wave");
+        for (int t0 = wave; t0 < kTiles; t0 += 2 * kFwdWaves) {
+            int s[2];
+            bool valid[2];
+            h8 x0[2][KQ0];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int t = t0 + k * kFwdWaves;
+                const int px = bx0 + 32 * (t % (kBoxBlockW / 32)) + c, py = by0 + t / (kBoxBlockW / 32);
+                valid[k] = px < d.image_w && py < d.image_h;
+                const int cx = min(px, d.image_w - 1), cy = min(py, d.image_h - 1);
+                s[k] = cy * d.image_w + cx;
+                // Position and mip as forward_kernel<..., Decode16> (pixel index s).
+                uint32_t st = mix_seed((uint32_t)s[k], d.seed);
+                const float jx = uniform01(st) - 0.5f;
+                const float jy = uniform01(st) - 0.5f;
+                const float zu = uniform01(st);
+                const float posx = clampf(fmaf(d.jitter, jx, (float)cx + 0.5f), 0.5f, (float)d.image_w - 0.5f);
+                const float posy = clampf(fmaf(d.jitter, jy, (float)cy + 0.5f), 0.5f, (float)d.image_h - 0.5f);
+                const float u = div_pow2(posx, (float)d.image_w, d.inv_w);
+                const float v = div_pow2(posy, (float)d.image_h, d.inv_h);
+                const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
+                sample_box16<KQ0>(gtab, tab, box, u, v, z, g, x0[k]);
+            }
 
-            h8 xh[HQ];
+            f16v out[2][1];
             {
-                f16v acc[HA];
-                layer_forward<KQ0, HA>(frags + S::fwd_off(0) * kWave, bias + S::bias_off(0), x0, acc, lane);
-                to_fragments<HQ, HA, true>(acc, xh);
+                h8 xh[2][HQ];
+                f16v acc[2][HA];
+                layer_forward2<KQ0, HA>(frags + S::fwd_off(0) * kWave, bias + S::bias_off(0), x0[0], x0[1], acc[0],
+                                        acc[1], lane);
+                to_fragments<HQ, HA, true>(acc[0], xh[0]);
+                to_fragments<HQ, HA, true>(acc[1], xh[1]);
 #pragma unroll
                 for (int l = 1; l < NH; ++l) {
-                    layer_forward<HQ, HA>(frags + S::fwd_off(l) * kWave, bias + S::bias_off(l), xh, acc, lane);
-                    to_fragments<HQ, HA, true>(acc, xh);
+                    layer_forward2<HQ, HA>(frags + S::fwd_off(l) * kWave, bias + S::bias_off(l), xh[0], xh[1], acc[0],
+                                           acc[1], lane);
+                    to_fragments<HQ, HA, true>(acc[0], xh[0]);
+                    to_fragments<HQ, HA, true>(acc[1], xh[1]);
                 }
+                layer_forward2<HQ, 1>(frags + S::fwd_off(L - 1) * kWave, bias + S::bias_off(L - 1), xh[0], xh[1],
+                                      out[0], out[1], lane);
             }
-            f16v out[1];
-            layer_forward<HQ, 1>(frags + S::fwd_off(L - 1) * kWave, bias + S::bias_off(L - 1), xh, out, lane);
-            if (!valid)
-                continue;
-            uint16_t *orow = d.out16 + (int64_t)s * d.out_stride;
             const bool quads = (d.out_stride & 3) == 0;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int o = 8 * j + 4 * g;
-                const f2 v0 = {out[0][4 * j], out[0][4 * j + 1]}, v1 = {out[0][4 * j + 2], out[0][4 * j + 3]};
-                const h2 h0 = __builtin_convertvector(v0, h2), h1 = __builtin_convertvector(v1, h2);
-                if (quads) {
-                    if (o < d.out_stride)
-                        *(uint2 *)(orow + o) = make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
-                } else {
-                    const _Float16 hv[4] = {h0[0], h0[1], h1[0], h1[1]};
+            for (int k = 0; k < 2; ++k) {
+                if (!valid[k])
+                    continue;
+                uint16_t *orow = d.out16 + (int64_t)s[k] * d.out_stride;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (o + r < d.out_stride)
-                            orow[o + r] = h_bits(hv[r]);
+                for (int j = 0; j < 2; ++j) {
+                    const int o = 8 * j + 4 * g;
+                    const f2 v0 = {out[k][0][4 * j], out[k][0][4 * j + 1]}, v1 = {out[k][0][4 * j + 2], out[k][0][4 * j + 3]};
+                    const h2 h0 = __builtin_convertvector(v0, h2), h1 = __builtin_convertvector(v1, h2);
+                    if (quads) {
+                        if (o < d.out_stride)
+                            *(uint2 *)(orow + o) = make_uint2(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1));
+                    } else {
+                        const _Float16 hv[4] = {h0[0], h0[1], h1[0], h1[1]};
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (o + r < d.out_stride)
+                                orow[o + r] = h_bits(hv[r]);
+                    }
                 }
             }
         }

@@ -189,6 +189,33 @@ __device__ __forceinline__ void layer_forward(const h8 *frags, const float *bias
     }
 }
 
+// One forward layer for two 32-sample tiles: each weight fragment read from LDS feeds the
+// MFMAs of both tiles, which also gives two independent accumulation chains.
+template <int KQ, int NA>
+__device__ __forceinline__ void layer_forward2(const h8 *frags, const float *bias, const h8 (&x0)[KQ],
+                                               const h8 (&x1)[KQ], f16v (&acc0)[NA], f16v (&acc1)[NA], int lane)
+{
+    const int g = lane >> 5;
+    const float4 *b4 = (const float4 *)(bias + 4 * g);
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 v = b4[8 * a + 2 * j];
+            acc0[a][4 * j] = acc1[a][4 * j] = v.x;
+            acc0[a][4 * j + 1] = acc1[a][4 * j + 1] = v.y;
+            acc0[a][4 * j + 2] = acc1[a][4 * j + 2] = v.z;
+            acc0[a][4 * j + 3] = acc1[a][4 * j + 3] = v.w;
+        }
+#pragma unroll
+        for (int q = 0; q < KQ; ++q) {
+            const h8 w = frags[(a * KQ + q) * kWave + lane];
+            acc0[a] = mfma32(w, x0[q], acc0[a]);
+            acc1[a] = mfma32(w, x1[q], acc1[a]);
+        }
+    }
+}
+
 // D tiles -> chained fp16 fragments, with optional ReLU (mlp.h:35-38). The ReLU is taken
 // after the conversion, as a signed 16-bit max with 0 on the pair (v_pk_max_i16): negative
 // halves and -0 have the sign bit set, so they become +0. fp16 rounding is monotone, so
