@@ -405,17 +405,20 @@ def test_codec_bit_exact(lib, O, w, h, c):
 
 # ---- decode from quantized latents ------------------------------------------------------------------
 
-@pytest.mark.parametrize("W,H,jitter,mip_min,mip_max", [
-    (96, 96, 1.0, 0.0, 3.0),
-    (100, 37, -1.5, 0.5, 6.0),   # ragged blocks, negative jitter, mips past the last one
-    (70, 20, 3.0, -1.0, 1.0),    # negative mip coordinates clamp to mip 0
-], ids=["96x96", "100x37", "70x20"])
-def test_decode_from_codec_latents(lib, O, W, H, jitter, mip_min, mip_max):
+@pytest.mark.parametrize("shape,W,H,jitter,mip_min,mip_max", [
+    ("c4", 96, 96, 1.0, 0.0, 3.0),
+    ("c4", 100, 37, -1.5, 0.5, 6.0),   # ragged blocks, negative jitter, mips past the last one
+    ("c4", 70, 20, 3.0, -1.0, 1.0),    # negative mip coordinates clamp to mip 0
+    ("c2", 100, 37, 1.0, 0.0, 3.0),    # the 2-grid network (32->64->64->9)
+], ids=["96x96", "100x37", "70x20", "c2-100x37"])
+def test_decode_from_codec_latents(lib, O, shape, W, H, jitter, mip_min, mip_max):
     import torch
-    say(f"case: decode c4 {W}x{H} jitter {jitter} z [{mip_min}, {mip_max})")
+    say(f"case: decode {shape} {W}x{H} jitter {jitter} z [{mip_min}, {mip_max})")
     rng = np.random.default_rng(50)
     C16 = 16
-    sizes = [(64, 5), (32, 5), (16, 4), (8, 3)]
+    sizes = [(64, 5), (32, 5), (16, 4), (8, 3)] if shape == "c4" else [(64, 5), (32, 5)]
+    net_sizes = [64, 64, 64, 64, 12] if shape == "c4" else [32, 64, 64, 9]
+    nout = net_sizes[-1]
     blobs, grids_np = [], []
     for size, mips in sizes:
         offs, total = P.codec_chain_layout(size, size, mips, C16)
@@ -427,11 +430,11 @@ def test_decode_from_codec_latents(lib, O, W, H, jitter, mip_min, mip_max):
             assert O.ntref_codec_encode(vals.ctypes.data, s, s, C16, blk.ctypes.data) == 0
             blob[offs[m]:offs[m] + blk.size] = blk
         blobs.append((size, mips, offs, blob))
-    net = P.make_network([64, 64, 64, 64, 12], rng=rng, init="xavier")
+    net = P.make_network(net_sizes, rng=rng, init="xavier")
 
     def dparams(blob_ptrs, netv, out_ptr):
         d = abi.nt_decode_params()
-        d.num_grids, d.channels = 4, C16
+        d.num_grids, d.channels = len(sizes), C16
         for i, (size, mips, offs, _) in enumerate(blobs):
             d.grids[i].width = d.grids[i].height = size
             d.grids[i].num_mips = mips
@@ -444,12 +447,12 @@ def test_decode_from_codec_latents(lib, O, W, H, jitter, mip_min, mip_max):
         d.output = C.cast(out_ptr, abi.u16p)
         return d
 
-    want = np.zeros(W * H * 12, np.uint16)
+    want = np.zeros(W * H * nout, np.uint16)
     dp = dparams([b[3].ctypes.data for b in blobs], net, want.ctypes.data)
     assert O.ntref_decode(C.byref(dp), 1) == 0
     gblobs = [torch.from_numpy(b[3]).cuda() for b in blobs]
     gnet = net.converted(True, "cuda")
-    gout = torch.zeros(W * H * 12, dtype=torch.int16, device="cuda")
+    gout = torch.zeros(W * H * nout, dtype=torch.int16, device="cuda")
     gp = dparams([g.data_ptr() for g in gblobs], gnet, gout.data_ptr())
     nt.check(lib.nt_decode(C.byref(gp), None))
     sync()
@@ -457,7 +460,7 @@ def test_decode_from_codec_latents(lib, O, W, H, jitter, mip_min, mip_max):
     assert rel_err(got, want.view(np.float16).astype(np.float32)) <= MLP_TOL
     # The two-pass decode (blocks expanded to fp16 texels first, then sampled from per-block
     # LDS boxes) gives the same bits.
-    say("case: decode c4 two-pass")
+    say(f"case: decode {shape} two-pass")
     nbytes = lib.nt_decode_workspace_bytes(C.byref(gp))
     assert nbytes > 0
     ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
