@@ -317,7 +317,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the path "
-              "shards by training region and is run per GPU — see DESIGN.md", file=sys.stderr)
+              "would shard by training region, one process per GPU, with one all-reduce of the "
+              "MLP gradient per step; only the one-GPU share is built", file=sys.stderr)
         sys.exit(2)
 
     import torch
