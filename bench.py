@@ -225,7 +225,8 @@ def train_entry(lib, nt, ev, cfg, steps, warmup, sample_mode=0, blocks=False):
               2: "train16_kernel<Shape<32,64,2>,16,2,false>",
               4: "train16_kernel<Shape<64,64,3>,16,1,false>"}[cfg]
     if blocks:
-        kernel = "train_kernel<Shape<16,32,2>,3,1>"
+        # The block phase: records expanded to texels, this kernel, gradients folded back.
+        kernel = "train16_kernel<Shape<16,32,2>,3,2,false> (BC6 block phase on expanded texels)"
     if sample_mode:
         kernel = f"train16_kernel<Shape<{'32' if cfg == 2 else '64'},64,{2 if cfg == 2 else 3}>,16,1,true>"
     if sample_mode:

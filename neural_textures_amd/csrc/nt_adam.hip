@@ -337,9 +337,13 @@ __global__ __launch_bounds__(256) void latent_adam_kernel(LatentAdamDesc d)
 // [0, nred) sum the train kernel's MLP-gradient partial rows, 64 parameters each (as
 // reduce_rows), and apply the network update to them (as net_adam_kernel: the same sum
 // g = grad + partials, then the same lazy update); the others run the latent update. The two
-// parts touch disjoint parameters. 256-thread workgroups: four row groups of 64 rows each
-// per parameter column, all of a thread's partial loads issued at once.
-constexpr int kOptCols = 64, kOptGroups = 4, kOptUnroll = 64;
+// parts touch disjoint parameters. 256-thread workgroups: the partial rows are summed as
+// reduce_rows sums them (kReduceRanges contiguous ranges, each in row order, then the range
+// sums in range order), each of the four thread groups taking four consecutive ranges with
+// all of their loads issued at once.
+constexpr int kOptCols = 64, kOptGroups = 4, kOptUnroll = 16;
+constexpr int kOptRangesPerGroup = kReduceRanges / kOptGroups;
+static_assert(kOptRangesPerGroup * kOptGroups == kReduceRanges, "ranges split evenly over the groups");
 
 __global__ __launch_bounds__(kOptCols *kOptGroups) void optimize_step_kernel(OptimizeStepDesc d)
 {
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(kOptCols *kOptGroups) void optimize_step_kernel(Opt
     }
     const ReduceDesc &r = d.red;
     const NetUpdateDesc &n = d.net;
-    __shared__ float part[kOptGroups][kOptCols];
+    __shared__ float part[kReduceRanges][kOptCols];
     const int col = threadIdx.x % kOptCols, grp = threadIdx.x / kOptCols;
     const int p0 = blockIdx.x * kOptCols, p = p0 + col;
     // Layers of this workgroup's 64 parameters (at most a few, uniform): the descriptor's
@@ -401,36 +405,43 @@ __global__ __launch_bounds__(kOptCols *kOptGroups) void optimize_step_kernel(Opt
             wbits = *wp;
         }
     }
-    const int per = (r.rows + kOptGroups - 1) / kOptGroups;
-    const int r0 = grp * per, r1 = min(r0 + per, r.rows);
-    float sum = 0.f;
+    const int per = (r.rows + kReduceRanges - 1) / kReduceRanges;
+    float sum[kOptRangesPerGroup] = {};
     if (p < r.P) {
         const float *c = r.partial + p;
-        for (int k0 = r0; k0 < r1; k0 += kOptUnroll) {
-            float v[kOptUnroll];
+        for (int k0 = 0; k0 < per; k0 += kOptUnroll) {
+            float v[kOptRangesPerGroup][kOptUnroll];
 #pragma unroll
-            for (int k = 0; k < kOptUnroll; ++k)
-                v[k] = k0 + k < r1 ? c[(int64_t)(k0 + k) * r.P] : 0.f;
+            for (int q = 0; q < kOptRangesPerGroup; ++q) {
+                const int r0 = (grp * kOptRangesPerGroup + q) * per, r1 = min(r0 + per, r.rows);
 #pragma unroll
-            for (int k = 0; k < kOptUnroll; ++k)
-                sum += v[k];
+                for (int k = 0; k < kOptUnroll; ++k)
+                    v[q][k] = r0 + k0 + k < r1 ? c[(int64_t)(r0 + k0 + k) * r.P] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < kOptRangesPerGroup; ++q)
+#pragma unroll
+                for (int k = 0; k < kOptUnroll; ++k)
+                    sum[q] += v[q][k];
         }
     }
-    part[grp][col] = sum;
+#pragma unroll
+    for (int q = 0; q < kOptRangesPerGroup; ++q)
+        part[grp * kOptRangesPerGroup + q][col] = sum[q];
     __syncthreads();
     if (grp != 0 || !gp)
         return;
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < kOptGroups; ++k)
+    for (int k = 0; k < kReduceRanges; ++k)
         s += part[k][col];
     const float g = gsum + s;
-    if (!active) {
+    if (!active || g == 0.f) {
+        // An inactive (padding) parameter only accumulates; a zero gradient skips the lazy
+        // update but the buffer still receives the sum, as reduce_rows writes it.
         *gp = g;
         return;
     }
-    if (g == 0.f)
-        return;
     const float w = adam_update(m1, m2, g, n.a, h2f(wbits));
     *m1p = m1;
     *m2p = m2;

@@ -294,6 +294,34 @@ UpdateLog *update_log(const nt_params *p)
     return (UpdateLog *)((uint8_t *)p->workspace + ((p->workspace_bytes - lb) & ~(size_t)15));
 }
 
+// Texel rectangle {x0, x1, y0, y1} of grid g (inclusive, before wrapping: x0 and y0 may
+// be negative, x1 and y1 past the grid) that holds every bilinear corner a train step's
+// positions reach; the whole grid where the positions are random or span it.
+void footprint_rect(const nt_params *p, const nt_grid &g, int (&rect)[4])
+{
+    if (p->sample_mode == NT_SAMPLES_RANDOM) {
+        rect[0] = rect[2] = 0;
+        rect[1] = g.width - 1;
+        rect[3] = g.height - 1;
+        return;
+    }
+    // Positions lie in [off, off + extent] texels of the image (jitter and clamping
+    // included); their footprints' corners at floor(pos * r - 0.5) + {0, 1}, with a texel
+    // of margin on each side for rounding.
+    const int rw = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
+    const double rx = (double)g.width / p->image_width, ry = (double)g.height / p->image_height;
+    const int rows = (int)(((int64_t)p->num_samples + rw - 1) / rw);
+    const int x0 = (int)std::floor(p->texel_offset_x * rx - 0.5) - 1;
+    const int x1 = (int)std::floor((double)(p->texel_offset_x + rw) * rx - 0.5) + 2;
+    const int y0 = (int)std::floor(p->texel_offset_y * ry - 0.5) - 1;
+    const int y1 = (int)std::floor((double)(p->texel_offset_y + rows) * ry - 0.5) + 2;
+    // Wider than the grid: the whole width (height) of it.
+    rect[0] = x1 - x0 + 1 >= g.width ? 0 : x0;
+    rect[1] = x1 - x0 + 1 >= g.width ? g.width - 1 : x1;
+    rect[2] = y1 - y0 + 1 >= g.height ? 0 : y0;
+    rect[3] = y1 - y0 + 1 >= g.height ? g.height - 1 : y1;
+}
+
 struct TrainPlan {
     int shape, nwg, chunks_per_wg, tiles_x, P;
     int fp_floats, fp_stride, tile_ok, scatter_mfma, scatter_split, scatter_off, w_rows, union_off;
@@ -305,6 +333,11 @@ struct TrainPlan {
     // The 16-channel unconstrained kernel (nt_train16.hip), when it applies.
     int use16, groups, rows;
     Train16Desc t16;
+    // The BC6 block phase on that kernel (Bc6PhaseDesc): block rectangles, and the
+    // workspace offsets of each grid's expanded texels and their gradients.
+    int bc6;
+    Bc6PhaseDesc bc6d;
+    size_t bc6_values_off[NT_MAX_GRIDS], bc6_grads_off[NT_MAX_GRIDS];
 };
 
 constexpr size_t kMaxLds = 160 * 1024;
@@ -535,6 +568,75 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     d.inv_samples = pow2_reciprocal(d.num_samples);
 }
 
+int floor_div4(int v) { return v >= 0 ? v / 4 : -((3 - v) / 4); }
+
+// The BC6 block phase (NT_BLOCK_FEATURES, NT_FINALIZE) of the reference network with region
+// sampling runs the fused unconstrained kernel on texels expanded from the block records
+// (Bc6PhaseDesc): the kernel is planned for the same step with 1-mip grids of the same
+// sizes whose texels live in the workspace, after its own partial rows. Sets plan->bc6.
+void plan_bc6_phase(const nt_params *p, TrainPlan *plan)
+{
+    plan->bc6 = 0;
+    if (plan->shape != kShapeRef || p->sample_mode != NT_SAMPLES_REGION || p->sample_mip != 0.f)
+        return;
+    const int C = p->latents.channels, G = p->latents.num_grids;
+    nt_params q = *p;
+    q.latent_update = NT_LATENT_DENSE;
+    for (int gi = 0; gi < G; ++gi) {
+        nt_grid &g = q.latents.grids[gi];
+        // Whole blocks only: the expansion and the fold address texels block by block.
+        if ((g.width & 3) || (g.height & 3))
+            return;
+        g.num_mips = 1;
+        g.mip_offset[0] = 0;
+        // Stand-ins for the workspace arrays (set at launch); 256-byte aligned like them.
+        g.values = g.grads = (float *)(uintptr_t)256;
+    }
+    TrainPlan t = *plan;
+    plan16(&q, NT_UNCONSTRAINED, &t);
+    if (!t.use16)
+        return;
+    *plan = t;
+    Bc6PhaseDesc &b = plan->bc6d;
+    b = Bc6PhaseDesc{};
+    b.G = G;
+    b.C = C;
+    size_t off = (plan->workspace + 255) & ~(size_t)255;
+    int64_t first = 0;
+    for (int gi = 0; gi < G; ++gi) {
+        const nt_grid &g = p->latents.grids[gi];
+        Bc6PhaseGrid &x = b.grid[gi];
+        x.w = g.width;
+        x.h = g.height;
+        x.nbu = g.width / 4;
+        x.nbv = g.height / 4;
+        int r[4];
+        footprint_rect(p, g, r);
+        x.bx0 = floor_div4(r[0]);
+        x.nbx = floor_div4(r[1]) - x.bx0 + 1;
+        if (x.nbx >= x.nbu) {
+            x.bx0 = 0;
+            x.nbx = x.nbu;
+        }
+        x.by0 = floor_div4(r[2]);
+        x.nby = floor_div4(r[3]) - x.by0 + 1;
+        if (x.nby >= x.nbv) {
+            x.by0 = 0;
+            x.nby = x.nbv;
+        }
+        x.first_block = first;
+        first += (int64_t)x.nbx * x.nby;
+        const size_t bytes = ((size_t)g.width * g.height * C * sizeof(float) + 255) & ~(size_t)255;
+        plan->bc6_values_off[gi] = off;
+        off += bytes;
+        plan->bc6_grads_off[gi] = off;
+        off += bytes;
+    }
+    b.total_blocks = first;
+    plan->workspace = off;
+    plan->bc6 = 1;
+}
+
 int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
 {
     if (!p)
@@ -664,7 +766,10 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         }
     }
     plan->rows = plan->nwg;
+    plan->bc6 = 0;
     plan16(p, type, plan);
+    if (type != NT_UNCONSTRAINED && !plan->use16)
+        plan_bc6_phase(p, plan);
     return NT_OK;
 }
 
@@ -811,6 +916,22 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
     hipStream_t s = (hipStream_t)stream;
     float *partial = (float *)(ws + plan.weight_bytes);
     hipError_t e;
+    Bc6PhaseDesc b6{};
+    if (plan.bc6) {
+        b6 = plan.bc6d;
+        const int C = p->latents.channels;
+        for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+            const nt_grid &g = p->latents.grids[gi];
+            Bc6PhaseGrid &x = b6.grid[gi];
+            x.params = g.block_params + g.block_offset[0] * (4 * C + 18);
+            x.grads = g.block_grads ? g.block_grads + g.block_offset[0] * (4 * C + 16) : nullptr;
+            x.values = (float *)(ws + plan.bc6_values_off[gi]);
+            x.tgrads = (float *)(ws + plan.bc6_grads_off[gi]);
+        }
+        e = launch_bc6_expand(b6, s);
+        if (e != hipSuccess)
+            return hip_status(e, "BC6 expansion launch");
+    }
     if (log && !(plan.use16 && type == NT_UNCONSTRAINED)) {
         // This kernel does not record its footprints: the optimizer updates every texel.
         e = launch_log_dense_step(log, s);
@@ -822,34 +943,21 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
         d.mlp = mlp_desc(&p->mlp);
         d.partial = partial;
         d.log = log;
-        for (int gi = 0; gi < NT_MAX_GRIDS && log; ++gi) {
+        if (plan.bc6) {
+            // The block phase trains on the expanded texels; the block Adam scans densely.
+            d.log = nullptr;
+            for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+                d.grid[gi].values = b6.grid[gi].values;
+                d.grid[gi].grads = b6.grid[gi].tgrads;
+            }
+        }
+        for (int gi = 0; gi < NT_MAX_GRIDS && d.log; ++gi) {
             if (gi >= p->latents.num_grids) {
                 d.rect[gi][0] = d.rect[gi][2] = 0;
                 d.rect[gi][1] = d.rect[gi][3] = -1;
                 continue;
             }
-            const nt_grid &g = p->latents.grids[gi];
-            if (d.random_texels) {
-                // Positions anywhere in the image: the whole grid.
-                d.rect[gi][0] = d.rect[gi][2] = 0;
-                d.rect[gi][1] = g.width - 1;
-                d.rect[gi][3] = g.height - 1;
-                continue;
-            }
-            // Positions lie in [off, off + extent] texels of the image (jitter and clamping
-            // included); their footprints' corners at floor(pos * r - 0.5) + {0, 1}, with a
-            // texel of margin on each side for rounding.
-            const double rx = (double)g.width / p->image_width, ry = (double)g.height / p->image_height;
-            const int rows = (int)(((int64_t)p->num_samples + d.region_w - 1) / d.region_w);
-            const int x0 = (int)std::floor(p->texel_offset_x * rx - 0.5) - 1;
-            const int x1 = (int)std::floor((double)(p->texel_offset_x + d.region_w) * rx - 0.5) + 2;
-            const int y0 = (int)std::floor(p->texel_offset_y * ry - 0.5) - 1;
-            const int y1 = (int)std::floor((double)(p->texel_offset_y + rows) * ry - 0.5) + 2;
-            // Wider than the grid: the whole width (height) of it.
-            d.rect[gi][0] = x1 - x0 + 1 >= g.width ? 0 : x0;
-            d.rect[gi][1] = x1 - x0 + 1 >= g.width ? g.width - 1 : x1;
-            d.rect[gi][2] = y1 - y0 + 1 >= g.height ? 0 : y0;
-            d.rect[gi][3] = y1 - y0 + 1 >= g.height ? g.height - 1 : y1;
+            footprint_rect(p, p->latents.grids[gi], d.rect[gi]);
         }
         {
             ProfileScope prof(s);
@@ -857,6 +965,11 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
         }
         if (e != hipSuccess)
             return hip_status(e, "train kernel launch");
+        if (plan.bc6 && type == NT_BLOCK_FEATURES) {
+            e = launch_bc6_fold(b6, s);
+            if (e != hipSuccess)
+                return hip_status(e, "BC6 fold launch");
+        }
     } else {
     TrainDesc d{};
     d.mlp = mlp_desc(&p->mlp);

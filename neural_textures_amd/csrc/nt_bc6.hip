@@ -233,4 +233,166 @@ hipError_t launch_bc6_init(const Bc6InitDesc &d, hipStream_t s)
     return hipGetLastError();
 }
 
+// ---- the BC6 block phase on the fused train kernel ------------------------------------
+
+// The grid of a launch-wide block number (grids take consecutive ranges of blocks).
+__device__ __forceinline__ int bc6_phase_grid(const Bc6PhaseDesc &d, int64_t b)
+{
+    int gi = 0;
+#pragma unroll
+    for (int k = 1; k < NT_MAX_GRIDS; ++k)
+        if (k < d.G && b >= d.grid[k].first_block)
+            gi = k;
+    return gi;
+}
+
+__device__ __forceinline__ int wrap_mod(int v, int n)
+{
+    const int r = v % n;
+    return r < 0 ? r + n : r;
+}
+
+// Expansion: one thread per texel of a block rectangle, numbered block by block and, in a
+// block, row-major, so that 16 consecutive threads share one record. Each texel's C values are the
+// reference's BC6 decode of its block (train.cu:240-261, DecompressBC6 :169-182), the same
+// function the per-sample gather applies; its gradients are cleared.
+template <int C>
+__global__ __launch_bounds__(256) void bc6_expand_kernel(Bc6PhaseDesc d)
+{
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t b = t >> 4;
+    if (b >= d.total_blocks)
+        return;
+    const Bc6PhaseGrid &g = d.grid[bc6_phase_grid(d, b)];
+    const int64_t lb = b - g.first_block;
+    const int bx = wrap_mod(g.bx0 + (int)(lb % g.nbx), g.nbu);
+    const int by = wrap_mod(g.by0 + (int)(lb / g.nbx), g.nbv);
+    const int pix = (int)(t & 15);
+    const float *rec = g.params + ((int64_t)by * g.nbu + bx) * (4 * C + 18);
+    const int partition = __float_as_int(rec[4 * C + 16]);
+    const int bits = bc6_mode_bits(__float_as_int(rec[4 * C + 17]));
+    const int part = (bc6_partition_mask(partition) >> pix) & 1;
+    const float xi = rec[4 * C + pix];
+    const int x = 4 * bx + (pix & 3), y = 4 * by + (pix >> 2);
+    const int64_t o = ((int64_t)y * g.w + x) * C;
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) {
+        g.values[o + ch] = bc6_decompress(rec[2 * part * C + ch], rec[(2 * part + 1) * C + ch], bits, xi);
+        g.tgrads[o + ch] = 0.f;
+    }
+}
+
+// Fold: one thread per block of the rectangle. The reference adds, for every corner that
+// lands on texel (pixel p) of a block, with feature gradient w * g per channel
+// (train.cu:405-455):
+//   dl_dy = ldexp(w g, hy - 24),   hy from y = q0 + 8 (q1 - q0) x_p  (that texel's channel)
+//   pixel index p:    += sum_ch dl_dy * 8 (q1 - q0)
+//   endpoints of p's partition, channel ch:  e0 += (1 - 8 x_p) (31/64) 2^(16 - bits) dl_dy,
+//                                            e1 += 8 x_p (31/64) 2^(16 - bits) dl_dy.
+// Every factor but w g depends on the texel and channel only, and ldexp by an integer is
+// exact, so the sums over corners equal these terms applied to the texel's gradient
+// G = sum w g (which the fused kernel accumulated) up to the order of the fp32 additions
+// (which the reference's atomics leave open as well). Texels with a zero gradient add
+// nothing; the block's record gradients are read, added to and written by this thread only.
+template <int C>
+__global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
+{
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= d.total_blocks)
+        return;
+    const Bc6PhaseGrid &g = d.grid[bc6_phase_grid(d, b)];
+    const int64_t lb = b - g.first_block;
+    const int bx = wrap_mod(g.bx0 + (int)(lb % g.nbx), g.nbu);
+    const int by = wrap_mod(g.by0 + (int)(lb / g.nbx), g.nbv);
+    float G[16][C];
+    bool any = false;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+        const int64_t o = ((int64_t)(4 * by + (p >> 2)) * g.w + 4 * bx + (p & 3)) * C;
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch) {
+            G[p][ch] = g.tgrads[o + ch];
+            any |= G[p][ch] != 0.f;
+        }
+    }
+    if (!any)
+        return;
+    const int64_t blk = (int64_t)by * g.nbu + bx;
+    const float *rec = g.params + blk * (4 * C + 18);
+    float *grec = g.grads + blk * (4 * C + 16);
+    const int mask = bc6_partition_mask(__float_as_int(rec[4 * C + 16]));
+    const int bits = bc6_mode_bits(__float_as_int(rec[4 * C + 17]));
+    const float deibar = ldexpf(31.f / 64.f, 16 - bits);
+    float q[4][C];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch)
+            q[e][ch] = bc6_unquantize(rec[e * C + ch], bits);
+    float de[4][C];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch)
+            de[e][ch] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+        bool touched = false;
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch)
+            touched |= G[p][ch] != 0.f;
+        if (!touched)
+            continue;
+        const int part = (mask >> p) & 1;
+        const float xi = rec[4 * C + p];
+        const float alpha = ldexpf(xi, 3);
+        float dl_dx = 0.f;
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch) {
+            const float q0 = part ? q[2][ch] : q[0][ch];
+            const float q1 = part ? q[3][ch] : q[1][ch];
+            const int hy = bc6_hy(bc6_y(q0, q1, xi));
+            const float dl_dy = ldexpf(G[p][ch], hy - 24);
+            dl_dx += dl_dy * ldexpf(q1 - q0, 3);
+            const float a0 = ((1.f - alpha) * deibar) * dl_dy;
+            const float a1 = (alpha * deibar) * dl_dy;
+            if (part) {
+                de[2][ch] += a0;
+                de[3][ch] += a1;
+            } else {
+                de[0][ch] += a0;
+                de[1][ch] += a1;
+            }
+        }
+        grec[4 * C + p] += dl_dx;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch)
+            if (de[e][ch] != 0.f)
+                grec[e * C + ch] += de[e][ch];
+}
+
+hipError_t launch_bc6_expand(const Bc6PhaseDesc &d, hipStream_t s)
+{
+    if (d.total_blocks <= 0)
+        return hipSuccess;
+    if (d.C != 3)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(bc6_expand_kernel<3>, dim3((unsigned)((d.total_blocks * 16 + 255) / 256)), dim3(256), 0, s,
+                       d);
+    return hipGetLastError();
+}
+
+hipError_t launch_bc6_fold(const Bc6PhaseDesc &d, hipStream_t s)
+{
+    if (d.total_blocks <= 0)
+        return hipSuccess;
+    if (d.C != 3)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(bc6_fold_kernel<3>, dim3((unsigned)((d.total_blocks + 255) / 256)), dim3(256), 0, s, d);
+    return hipGetLastError();
+}
+
 } // namespace ntk

@@ -175,6 +175,11 @@ struct PrepDesc {
 };
 
 // Gradient reduction descriptor: partial[rows][P] -> mlp gradients.
+// The MLP-gradient partial rows are summed as kReduceRanges contiguous ranges of
+// ceil(rows / kReduceRanges) rows, each in row order, then the range sums in range order.
+// reduce_rows and the fused optimizer both follow this split, so they give the same bits.
+constexpr int kReduceRanges = 16;
+
 struct ReduceDesc {
     const float *partial;
     int rows, P;
@@ -217,6 +222,28 @@ struct Bc6InitDesc {
     float *blocks[kMaxExpandLevels];       // the level's first block record
     int w[kMaxExpandLevels], h[kMaxExpandLevels], nbu[kMaxExpandLevels];
     int64_t start[kMaxExpandLevels + 1];
+};
+
+// BC6 block phase on the fused train kernel (NT_BLOCK_FEATURES, NT_FINALIZE with the
+// reference network's four 3-channel grids, region sampling). Per grid, the block records
+// of mip 0 under a rectangle of blocks that holds every footprint of the step are expanded
+// to fp32 texels in the workspace ([y * w + x][C], the unconstrained layout; their
+// gradients cleared); the fused unconstrained kernel trains on those texels; the fold then
+// turns each block's texel gradients into its record's endpoint and pixel-index gradients
+// (train.cu:373-458), which are linear in the texel gradient.
+struct Bc6PhaseGrid {
+    const float *params; // mip-0 block records, 4C + 18 floats each
+    float *grads;        // mip-0 block-gradient records, 4C + 16 floats each
+    float *values;       // expanded texels (workspace), w * h * C floats
+    float *tgrads;       // their gradients (workspace)
+    int w, h, nbu, nbv;  // texels; blocks per row and column
+    int bx0, by0, nbx, nby; // block rectangle: origin (may lie outside the grid: wraps), size
+    int64_t first_block;    // first block of this grid in the launch's numbering
+};
+struct Bc6PhaseDesc {
+    Bc6PhaseGrid grid[NT_MAX_GRIDS];
+    int G, C;
+    int64_t total_blocks;
 };
 
 // Second pass of the two-pass decode, LDS-staged: a workgroup decodes blocks of
@@ -397,5 +424,8 @@ hipError_t launch_codec_decode(const uint8_t *blocks, int w, int h, int C, float
                                hipStream_t s);
 hipError_t launch_codec_expand(const CodecExpandDesc &d, hipStream_t s);
 hipError_t launch_bc6_init(const Bc6InitDesc &d, hipStream_t s);
+// The expansion before and the fold after the fused kernel of the BC6 block phase.
+hipError_t launch_bc6_expand(const Bc6PhaseDesc &d, hipStream_t s);
+hipError_t launch_bc6_fold(const Bc6PhaseDesc &d, hipStream_t s);
 
 } // namespace ntk

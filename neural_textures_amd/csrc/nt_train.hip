@@ -1133,7 +1133,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 // group's rows of one parameter in row order (all loads issued before the adds: every wave
 // load is 256 contiguous bytes of one row), then wave 0 adds the 16 group sums in group
 // order. The same bits on every run.
-constexpr int kReduceCols = 64, kReduceGroups = 16, kReduceUnroll = 16;
+constexpr int kReduceCols = 64, kReduceGroups = kReduceRanges, kReduceUnroll = 16;
 __global__ __launch_bounds__(kReduceCols *kReduceGroups) void reduce_rows(ReduceDesc d)
 {
     __shared__ float part[kReduceGroups][kReduceCols];

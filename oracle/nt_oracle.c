@@ -90,6 +90,17 @@ uint16_t ntref_f16_add(uint16_t a, uint16_t b)
 
 static double h2d(uint16_t h) { return (double)ntref_f16_to_f32(h); }
 
+/* With this switch on, the MLP's forward sums and its backward dY W^T sums accumulate in
+ * fp32 (in index order, the fp16 products exact) instead of float64: a second, equally
+ * valid accumulation order, with which the tests measure how sensitive each gradient
+ * element is to the order of the fp32 sums (the GPU's MFMA order is a third). */
+static int g_mlp_accum_f32 = 0;
+
+void ntref_set_mlp_accum_f32(int on)
+{
+    g_mlp_accum_f32 = on != 0;
+}
+
 /* ---- RNG and sample positions (train.cu:37-58, 818-844) --------------------------- */
 
 uint32_t ntref_xorshift32(uint32_t *state)
@@ -699,10 +710,19 @@ void ntref_mlp_forward_one(const nt_mlp *mlp, const uint16_t *in, uint16_t *acts
         }
         const uint16_t *W = mlp->weights[l];
         for (int n = 0; n < pout; ++n) {
-            double acc = n < mlp->sizes[l + 1] ? h2d(mlp->biases[l][n]) : 0.0;
-            for (int k = 0; k < pin; ++k)
-                acc += h2d(cur[k]) * h2d(W[n * pin + k]);
-            float y = (float)acc;
+            float y;
+            if (g_mlp_accum_f32) {
+                /* products of two fp16 values are exact in fp32 */
+                float a = n < mlp->sizes[l + 1] ? ntref_f16_to_f32(mlp->biases[l][n]) : 0.f;
+                for (int k = 0; k < pin; ++k)
+                    a += ntref_f16_to_f32(cur[k]) * ntref_f16_to_f32(W[n * pin + k]);
+                y = a;
+            } else {
+                double acc = n < mlp->sizes[l + 1] ? h2d(mlp->biases[l][n]) : 0.0;
+                for (int k = 0; k < pin; ++k)
+                    acc += h2d(cur[k]) * h2d(W[n * pin + k]);
+                y = (float)acc;
+            }
             if (l < L - 1 && !(y > 0.f))
                 y = 0.f; /* ReLU on hidden layers (mlp.h:35-38) */
             nxt[n] = ntref_f32_to_f16(y);
@@ -732,10 +752,18 @@ void ntref_mlp_backward_one(const nt_mlp *mlp, const uint16_t *acts, const uint1
                     dw[l][n * pin + k] += h2d(x[k]) * d;
         }
         for (int k = 0; k < pin; ++k) { /* dY W^T, then ReLU mask (mlp.h:243-247) */
-            double s = 0.0;
-            for (int n = 0; n < pout; ++n)
-                s += h2d(W[n * pin + k]) * h2d(dy[n]);
-            float g = (float)s;
+            float g;
+            if (g_mlp_accum_f32) {
+                float a = 0.f;
+                for (int n = 0; n < pout; ++n)
+                    a += ntref_f16_to_f32(W[n * pin + k]) * ntref_f16_to_f32(dy[n]);
+                g = a;
+            } else {
+                double s = 0.0;
+                for (int n = 0; n < pout; ++n)
+                    s += h2d(W[n * pin + k]) * h2d(dy[n]);
+                g = (float)s;
+            }
             if (l > 0 && !(ntref_f16_to_f32(x[k]) > 0.f))
                 g = 0.f;
             dx[k] = ntref_f32_to_f16(g);
@@ -800,6 +828,20 @@ int ntref_train_intermediates(const nt_params *p, int type, uint16_t *features, 
     return NT_OK;
 }
 
+/* With this switch on, ntref_train_step rounds each warp's weight-gradient partial (the sum
+ * over its 32 consecutive samples of x (x) dy) to fp16 before adding it to the total, as the
+ * reference keeps the warp's outer product as __half2 registers before the fp32 atomics
+ * (mlp.h:166-173, 249-254). How tcnn accumulates inside the outer product is not visible in
+ * the reference; the partial is taken exactly and rounded once. Off (the default), the
+ * partials are summed in double. Bias gradients are fp32 sums of fp16 dy in both modes
+ * (SumRows, mlp.h:101-153). */
+static int g_dw_partial_fp16 = 0;
+
+void ntref_set_dw_partial_fp16(int on)
+{
+    g_dw_partial_fp16 = on != 0;
+}
+
 int ntref_train_step(const nt_params *p, int type, int num_threads)
 {
     if (!mlp_valid(&p->mlp) || p->num_samples <= 0)
@@ -828,32 +870,48 @@ int ntref_train_step(const nt_params *p, int type, int num_threads)
 #ifdef _OPENMP
         tid = omp_get_thread_num();
 #endif
-        double *dw[NT_MAX_LAYERS], *db[NT_MAX_LAYERS];
+        double *dw[NT_MAX_LAYERS], *db[NT_MAX_LAYERS], *wdw[NT_MAX_LAYERS];
+        /* warp partials of the weight gradients, when they are rounded to fp16 */
+        double *wbuf = g_dw_partial_fp16 ? (double *)malloc(per * sizeof(double)) : NULL;
         for (int l = 0; l < L; ++l) {
             dw[l] = acc + per * (size_t)tid + off_w[l];
             db[l] = acc + per * (size_t)tid + off_b[l];
+            wdw[l] = wbuf ? wbuf + off_w[l] : dw[l];
         }
+        const int nwarp = (p->num_samples + 31) / 32;
 #pragma omp for schedule(static)
-        for (int i = 0; i < p->num_samples; ++i) {
-            float uvz[3], expected[16], weights[16];
-            uint16_t f[MAXW], acts[NT_MAX_LAYERS * MAXW], out[16], dy[16], din[MAXW];
-            ntref_sample_uvz(p, (uint32_t)i, uvz);
-            sample_features(p, type, uvz, f);
-            ntref_expected_values(p, uvz, expected, weights);
-            ntref_mlp_forward_one(m, f, acts, out);
-            loss_gradient(p, out, expected, weights, dy);
-            ntref_mlp_backward_one(m, acts, dy, dw, db, din);
-            if (type == NT_UNCONSTRAINED) {
-                scatter_unconstrained(&p->latents, uvz, din, nt > 1);
-            } else if (type == NT_BLOCK_FEATURES) {
-                if (nt > 1) {
+        for (int w = 0; w < nwarp; ++w) {
+            if (wbuf)
+                memset(wbuf, 0, per * sizeof(double));
+            const int i1 = 32 * w + 32 < p->num_samples ? 32 * w + 32 : p->num_samples;
+            for (int i = 32 * w; i < i1; ++i) {
+                float uvz[3], expected[16], weights[16];
+                uint16_t f[MAXW], acts[NT_MAX_LAYERS * MAXW], out[16], dy[16], din[MAXW];
+                ntref_sample_uvz(p, (uint32_t)i, uvz);
+                sample_features(p, type, uvz, f);
+                ntref_expected_values(p, uvz, expected, weights);
+                ntref_mlp_forward_one(m, f, acts, out);
+                loss_gradient(p, out, expected, weights, dy);
+                ntref_mlp_backward_one(m, acts, dy, wdw, db, din);
+                if (type == NT_UNCONSTRAINED) {
+                    scatter_unconstrained(&p->latents, uvz, din, nt > 1);
+                } else if (type == NT_BLOCK_FEATURES) {
+                    if (nt > 1) {
 #pragma omp critical
-                    scatter_bc6(&p->latents, uvz, din);
-                } else {
-                    scatter_bc6(&p->latents, uvz, din);
+                        scatter_bc6(&p->latents, uvz, din);
+                    } else {
+                        scatter_bc6(&p->latents, uvz, din);
+                    }
                 }
             }
+            if (wbuf)
+                for (int l = 0; l < L; ++l) {
+                    const size_t nw = (size_t)PAD16(m->sizes[l]) * PAD16(m->sizes[l + 1]);
+                    for (size_t k = 0; k < nw; ++k)
+                        dw[l][k] += h2d(f64_to_f16(wdw[l][k]));
+                }
         }
+        free(wbuf);
     }
     for (int t = 1; t < nt; ++t)
         for (size_t i = 0; i < per; ++i)

@@ -105,6 +105,13 @@ void ntref_mlp_backward_one(const nt_mlp *mlp, const uint16_t *acts, const uint1
 
 /* ---- whole passes (mirroring the C ABI) --------------------------------------------- */
 int ntref_train_step(const nt_params *p, int type, int num_threads);
+/* 1: ntref_train_step rounds each 32-sample weight-gradient partial to fp16 before summing
+ * (the reference's __half2 warp partials, mlp.h:166-173); 0 (default): double sums. */
+void ntref_set_dw_partial_fp16(int on);
+/* 1: the MLP's forward and dY W^T sums accumulate in fp32 (index order); 0 (default): in
+ * float64. Tests use the difference between the two as each element's sensitivity to the
+ * order of fp32 sums. */
+void ntref_set_mlp_accum_f32(int on);
 int ntref_optimize_network(const nt_params *p);
 int ntref_optimize_latents(const nt_params *p, int type);
 int ntref_inference(const nt_params *p);

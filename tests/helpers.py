@@ -83,6 +83,56 @@ def rel_err(a, b):
     return float(np.linalg.norm(a - b) / den) if den > 0 else float(np.linalg.norm(a))
 
 
+def assert_close(got, want, name, alt=None, tol=1e-2, floor=1e-3, outliers=1e-4, loose=1e-2):
+    """The MLP-tolerance bar, norm-wise and per element.
+
+    Norm-wise: ||got - want|| <= tol * ||want|| over the whole buffer. Per element:
+    |got - want| <= tol * |want| + floor * max|want| + 2 |alt - want| (the strict bound), so
+    that a miss confined to a few hundred elements (a wrap column, a tile seam, one fallback
+    path) fails even where it moves the norm of a large buffer by little.
+
+    `alt` is the oracle's result for the same step with its MLP sums accumulated in fp32
+    instead of float64 (ntref_set_mlp_accum_f32): an element that a one-ulp fp16 rounding
+    upstream moves (a pre-activation at zero that flips a ReLU mask, a loss gradient rounded
+    the other way) differs between the two, and twice that spread is its own allowance for
+    the GPU's third accumulation order. Beyond it, at most max(8, outliers * n) elements may
+    leave the strict bound, and none the loose one (loose instead of floor). A failure
+    names the worst element by its index in the buffer's own shape (texel, channel)."""
+    a = np.asarray(to_np(got), np.float64)
+    b = np.asarray(to_np(want), np.float64).reshape(a.shape)
+    e = rel_err(a, b)
+    assert e <= tol, f"{name}: norm-wise relative error {e:.3e} > {tol}"
+    if b.size == 0:
+        return
+    m = float(np.abs(b).max())
+    diff = np.abs(a - b)
+    spread = 0.0 if alt is None else 2.0 * np.abs(np.asarray(to_np(alt), np.float64).reshape(a.shape) - b)
+
+    def worst(bound):
+        excess = diff - bound
+        i = int(np.argmax(excess))
+        idx = tuple(int(k) for k in np.unravel_index(i, a.shape))
+        return (int(np.count_nonzero(excess > 0)),
+                f"worst at index {idx}: got {a.flat[i]:.6e}, ref {b.flat[i]:.6e}, bound {bound.flat[i]:.3e} "
+                f"(max|ref| {m:.3e})")
+
+    n_loose, msg = worst(tol * np.abs(b) + loose * m + spread)
+    assert n_loose == 0, f"{name}: {n_loose} element(s) outside tol*|ref| + {loose}*max|ref| + spread; {msg}"
+    n_strict, msg = worst(tol * np.abs(b) + floor * m + spread)
+    allowed = max(8, int(outliers * b.size))
+    assert n_strict <= allowed, (f"{name}: {n_strict} element(s) (> {allowed}) outside tol*|ref| + "
+                                 f"{floor}*max|ref| + spread; {msg}")
+
+
+def oracle_step(O, st, ktype, threads=1, accum_f32=False):
+    """ntref_train_step on `st`, with the MLP sums in fp32 when accum_f32."""
+    O.ntref_set_mlp_accum_f32(1 if accum_f32 else 0)
+    try:
+        assert O.ntref_train_step(C.byref(st.params()), ktype, threads) == 0
+    finally:
+        O.ntref_set_mlp_accum_f32(0)
+
+
 def to_np(x):
     return x if isinstance(x, np.ndarray) else x.detach().cpu().numpy()
 

@@ -50,6 +50,8 @@ SIGNATURES = {
     "ntref_decode": (C.c_int, [P(abi.nt_decode_params), C.c_int]),
     "ntref_decode_rect": (C.c_int, [P(abi.nt_decode_params), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "ntref_set_threads": (None, [C.c_int]),
+    "ntref_set_dw_partial_fp16": (None, [C.c_int]),
+    "ntref_set_mlp_accum_f32": (None, [C.c_int]),
     "ntref_bc6_value_to_y": (C.c_float, [C.c_float]),
     "ntref_bc6_fit_subset": (C.c_float, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                          C.c_void_p, C.c_void_p, C.c_void_p]),

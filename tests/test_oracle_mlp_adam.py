@@ -163,6 +163,59 @@ def test_weight_gradient_is_outer_product_and_padding_stays_zero():
     assert np.all(np.isfinite(dw0))
 
 
+def _one_layer_state(num_samples, seed):
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from helpers import make_state
+    st = make_state("c2", image=64, region=(16, (num_samples + 15) // 16), offset=(9, 21), seed=seed)
+    st.num_samples = num_samples
+    # one layer 32 -> 9: its input is the sampled features, so the weight gradient is the
+    # outer product of quantities ntref_train_intermediates returns
+    st.net = P.make_network([32, 9], used_outputs=9, rng=np.random.default_rng(seed), init="xavier")
+    return st
+
+
+def _dw_from_intermediates(st, fp16_partials):
+    """Sum over samples of f (x) dy (fp16 features and loss gradients from the oracle), in
+    sample order in float64; with fp16_partials, each run of 32 consecutive samples is summed
+    alone and rounded to fp16 (numpy's binary16, nearest-even) before it is added."""
+    n = st.num_samples
+    f = np.zeros(n * 32, np.uint16)
+    dy = np.zeros(n * 16, np.uint16)
+    assert O.ntref_train_intermediates(C.byref(st.params()), 0, f.ctypes.data, dy.ctypes.data, None) == 0
+    f = f.view(np.float16).astype(np.float64).reshape(n, 32)
+    dy = dy.view(np.float16).astype(np.float64).reshape(n, 16)
+    total = np.zeros((16, 32))
+    for w0 in range(0, n, 32):
+        part = np.zeros((16, 32))
+        for s in range(w0, min(w0 + 32, n)):
+            part += np.outer(dy[s], f[s])
+        total += part.astype(np.float16).astype(np.float64) if fp16_partials else part
+    return total.astype(np.float32).reshape(-1)
+
+
+def test_dw_partials_rounded_to_fp16_per_warp():
+    """ntref_set_dw_partial_fp16: each 32-sample warp's weight-gradient partial is rounded to
+    fp16 before the sum (the reference's __half2 outer-product registers, mlp.h:166-173).
+    Pinned on a one-layer network, whose weight gradient is the outer product of the
+    features and loss gradients ntref_train_intermediates returns, over 2.5 warps (a ragged
+    last warp): bit-exact against the sum restated in numpy in both modes, and the two modes
+    differ. Rounding per sample, rounding the total, or another warp size fails it."""
+    for fp16 in (0, 1):
+        st = _one_layer_state(80, seed=31)
+        O.ntref_set_dw_partial_fp16(fp16)
+        try:
+            assert O.ntref_train_step(C.byref(st.params()), 0, 1) == 0
+        finally:
+            O.ntref_set_dw_partial_fp16(0)
+        want = _dw_from_intermediates(st, bool(fp16))
+        assert np.array_equal(st.net.weight_grads[0], want), fp16
+        if fp16:
+            assert not np.array_equal(want, _dw_from_intermediates(st, False))
+        # the bias gradient is the fp32 sum of fp16 dy either way
+        assert np.count_nonzero(st.net.bias_grads[0]) > 0
+
+
 # ---- lazy Adam (train.cu:521-816) -----------------------------------------------------
 
 def _adam_state(step, grads_w0):
