@@ -148,9 +148,9 @@ def bench_train(lib, nt, ev, cfg, steps, warmup, sample_mode=0, blocks=False):
     device = "cuda:0"
     st = build_config(device, cfg)
     st.sample_mode = sample_mode
-    # The optimizer visits the 64-texel runs the train step marked (same results as the
-    # reference's dense scan, which the tests check); block records are scanned densely.
-    st.latent_update = abi.NT_LATENT_DENSE if blocks else abi.NT_LATENT_TOUCHED
+    # The optimizer visits the texel (or block-record) rectangles the train step logged
+    # (same results as the reference's dense scan, which the tests check).
+    st.latent_update = abi.NT_LATENT_TOUCHED
     ktype = abi.NT_BLOCK_FEATURES if blocks else abi.NT_UNCONSTRAINED
     if blocks:
         for g in st.grids:
@@ -642,8 +642,8 @@ def main():
             e["workload"] = ("the reference's own network in its BC6 block phase (NT_BLOCK_FEATURES, "
                              "main.cpp:1052-1060; not a BASELINE config): BCf-2k grids 3ch@2048^2..256^2 "
                              "as BC6 block records initialised by nt_bc6_init; 262,144 jittered samples of "
-                             "a 512^2 region of a 2048^2x9 target; MLP 12-32-32-16 fp16; Adam on the network "
-                             "and on every block record")
+                             "a 512^2 region of a 2048^2x9 target; MLP 12-32-32-16 fp16; lazy Adam on the "
+                             "network and on the block records (touched rectangles)")
             del st
         elif w == "c2r":
             st, e = train_entry(lib, nt, ev, 2, 20, 5, sample_mode=1)

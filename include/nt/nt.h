@@ -92,18 +92,22 @@ typedef enum nt_sample_mode {
 } nt_sample_mode;
 
 /*
- * What nt_optimize_latents (NT_UNCONSTRAINED) visits. NT_LATENT_DENSE is the reference's
- * (train.cu:764-803): every texel of every mip, lazy per value. NT_LATENT_TOUCHED (no
- * reference counterpart, same results): the last 256 bytes of params->workspace hold an
+ * What nt_optimize_latents visits. NT_LATENT_DENSE is the reference's (train.cu:764-803,
+ * 641-679): every texel (or block record) of every mip, lazy per value. NT_LATENT_TOUCHED
+ * (no reference counterpart, same results): the last 256 bytes of params->workspace hold an
  * update log. A train step of the 16-channel kernel records there the texel rectangle of
- * each grid that its samples' bilinear footprints can reach; when exactly one such step was
- * logged since the last optimizer call, nt_optimize_latents updates only those rectangles
- * (lazy per value as before), and every texel otherwise (several steps accumulated, another
- * kernel, a fresh workspace). Texels outside the rectangles hold zero gradients, which the
- * lazy rule skips, so the update is the same; this holds when every gradient since the last
- * optimizer call came from nt_train_step calls with this workspace (a caller that writes
- * latent gradients itself uses NT_LATENT_DENSE). A fresh workspace needs no
- * initialisation. nt_train_step_static keeps no log and refuses NT_LATENT_TOUCHED.
+ * each grid that its samples' bilinear footprints can reach, and a BC6-phase step
+ * (NT_BLOCK_FEATURES) of the reference network with region sampling the rectangle of mip-0
+ * block records under them; when exactly one such step was logged since the last optimizer
+ * call and the optimizer's kernel type matches (texels for NT_UNCONSTRAINED, blocks
+ * otherwise), nt_optimize_latents updates only those rectangles (lazy per value as before),
+ * and everything otherwise (several steps accumulated, another kernel, a fresh workspace).
+ * Values outside the rectangles hold zero gradients, which the lazy rule skips, so the
+ * update is the same; this holds when every gradient since the last optimizer call came
+ * from nt_train_step calls with this workspace (a caller that writes latent gradients itself
+ * uses NT_LATENT_DENSE). A fresh workspace needs no initialisation. NT_LATENT_TOUCHED needs
+ * params->workspace in nt_optimize_latents too. nt_train_step_static keeps no log and
+ * refuses NT_LATENT_TOUCHED.
  */
 typedef enum nt_latent_update {
     NT_LATENT_DENSE = 0,
@@ -273,9 +277,11 @@ int nt_train_step(const nt_params *params, nt_kernel_type type, void *stream);
 
 /*
  * nt_train_step without a workspace: the same kernels, with their scratch (the per-workgroup
- * MLP-gradient partials, and the prepared weight image of the general kernel) in a static
- * device array of nt_train_static_scratch_bytes() = 32 MiB that the library holds on every
- * GPU it runs on until the process ends. params->workspace is ignored. No reference
+ * MLP-gradient partials, the prepared weight image of the general kernel, and the texels the
+ * BC6 block phase expands) in a static device array of nt_train_static_scratch_bytes() =
+ * 32 MiB. The array is part of the library's code object: it is reserved on every GPU on
+ * which the process loads the library (any nt_* kernel launch there), whether or not this
+ * entry point is ever called, and held until the process ends. params->workspace is ignored. No reference
  * counterpart: this entry point is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc); it calls
  * no allocating routine. A step whose scratch exceeds the array fails with

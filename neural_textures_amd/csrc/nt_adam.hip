@@ -294,7 +294,7 @@ __device__ void latent_adam_body(const LatentAdamDesc &d, int bid, int nb, int t
         const UpdateLog *log = d.log;
         const bool valid = log->magic == kUpdateLogMagic;
         const uint32_t count = valid ? log->count : 0u;
-        const bool rects = valid && count == 1u && (d.C == 16 || d.C == 3);
+        const bool rects = valid && count == 1u && log->kind == kUpdateLogTexels && (d.C == 16 || d.C == 3);
         if (rects) {
             int32_t rect[NT_MAX_GRIDS][4];
 #pragma unroll
@@ -461,10 +461,67 @@ hipError_t launch_optimize_step(const OptimizeStepDesc &d0, hipStream_t s)
     return hipGetLastError();
 }
 
+// Lazy Adam of one float of a block record: `e` of the gradient record at g (rec floats)
+// and of the parameter record at w (rec + 2 floats).
+__device__ __forceinline__ void block_adam_float(const LatentAdamDesc &d, float *w, float *g, float *m1, float *m2)
+{
+    const float gs = *g;
+    if (gs == 0.f)
+        return;
+    float a1 = *m1, a2 = *m2;
+    *w = adam_update(a1, a2, gs, d.a, *w);
+    *m1 = a1;
+    *m2 = a2;
+    *g = 0.f;
+}
+
 // BC6 block records (OptimizeFeatureBlock, train.cu:641-679): every float of the
-// parameter record except the trailing partition/mode pair.
+// parameter record except the trailing partition/mode pair. With NT_LATENT_TOUCHED and a
+// log of exactly one BC6-phase train step, only the mip-0 blocks of the logged rectangles
+// are visited (every other record holds zero gradients, which the lazy rule skips), the
+// rectangles' records one after another, each in consecutive floats.
 __global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
 {
+    if (d.log) {
+        const UpdateLog *log = d.log;
+        const bool valid = log->magic == kUpdateLogMagic;
+        const uint32_t count = valid ? log->count : 0u;
+        const bool rects = valid && count == 1u && log->kind == kUpdateLogBlocks;
+        if (rects) {
+            const int rec = d.rec;
+            int64_t start[NT_MAX_GRIDS + 1];
+            int r[NT_MAX_GRIDS][4];
+            start[0] = 0;
+#pragma unroll
+            for (int s = 0; s < NT_MAX_GRIDS; ++s) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    r[s][k] = __builtin_amdgcn_readfirstlane(log->rect[s][k]);
+                const bool on = s < d.nseg;
+                start[s + 1] = start[s] + (on ? (int64_t)(r[s][1] - r[s][0] + 1) * (r[s][3] - r[s][2] + 1) * rec : 0);
+            }
+            const int64_t total = start[NT_MAX_GRIDS];
+            for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+                int s = 0;
+#pragma unroll
+                for (int q = 1; q < NT_MAX_GRIDS; ++q)
+                    s = i >= start[q] && q < d.nseg ? q : s;
+                const int64_t local = i - start[s];
+                const int64_t rb = local / rec;
+                const int e = (int)(local - rb * rec);
+                const int nbx = r[s][1] - r[s][0] + 1;
+                const int bx = wrap_coord(r[s][0] + (int)(rb % nbx), d.gw[s]);
+                const int by = wrap_coord(r[s][2] + (int)(rb / nbx), d.gh[s]);
+                const int64_t blk = (int64_t)by * d.gw[s] + bx;
+                block_adam_float(d, d.w[s] + blk * (rec + 2) + e, d.g[s] + blk * rec + e, d.m1[s] + blk * rec + e,
+                                 d.m2[s] + blk * rec + e);
+            }
+        }
+        if (valid && blockIdx.x == 0 && threadIdx.x == 0)
+            d.log->consumed = count;
+        if (rects)
+            return;
+    }
     // A workgroup takes 256 records at a time (segment starts are whole spans, so the
     // records are of one grid) and spreads their rec * 256 floats over its threads, each
     // array read and written in consecutive floats.

@@ -916,6 +916,7 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
     hipStream_t s = (hipStream_t)stream;
     float *partial = (float *)(ws + plan.weight_bytes);
     hipError_t e;
+    const bool bc6_log = plan.bc6 && type == NT_BLOCK_FEATURES;
     Bc6PhaseDesc b6{};
     if (plan.bc6) {
         b6 = plan.bc6d;
@@ -928,11 +929,21 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
             x.values = (float *)(ws + plan.bc6_values_off[gi]);
             x.tgrads = (float *)(ws + plan.bc6_grads_off[gi]);
         }
+        // The fold logs the block rectangles (BLOCK_FEATURES; other types log a dense step).
+        b6.log = bc6_log ? log : nullptr;
+        for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
+            const Bc6PhaseGrid &x = b6.grid[gi];
+            const bool on = gi < p->latents.num_grids;
+            b6.rect[gi][0] = on ? x.bx0 : 0;
+            b6.rect[gi][1] = on ? x.bx0 + x.nbx - 1 : -1;
+            b6.rect[gi][2] = on ? x.by0 : 0;
+            b6.rect[gi][3] = on ? x.by0 + x.nby - 1 : -1;
+        }
         e = launch_bc6_expand(b6, s);
         if (e != hipSuccess)
             return hip_status(e, "BC6 expansion launch");
     }
-    if (log && !(plan.use16 && type == NT_UNCONSTRAINED)) {
+    if (log && !(plan.use16 && type == NT_UNCONSTRAINED) && !bc6_log) {
         // This kernel does not record its footprints: the optimizer updates every texel.
         e = launch_log_dense_step(log, s);
         if (e != hipSuccess)
@@ -1211,7 +1222,7 @@ static int latent_adam_desc(const nt_params *p, nt_kernel_type type, LatentAdamD
     const bool blocks = type != NT_UNCONSTRAINED; // FINALIZE optimizes blocks too (train.cu:1018-1025)
     if (p->latent_update != NT_LATENT_DENSE && p->latent_update != NT_LATENT_TOUCHED)
         return fail(NT_ERR_INVALID_ARGUMENT, "latent_update %d", p->latent_update);
-    const bool touched = !blocks && p->latent_update == NT_LATENT_TOUCHED;
+    const bool touched = p->latent_update == NT_LATENT_TOUCHED;
     UpdateLog *log = touched ? update_log(p) : nullptr;
     if (touched && !log)
         return fail(NT_ERR_WORKSPACE, "NT_LATENT_TOUCHED needs the train step's workspace");
@@ -1270,8 +1281,10 @@ static int latent_adam_desc(const nt_params *p, nt_kernel_type type, LatentAdamD
         d.log = log;
         d.C = C;
         for (int gi = 0; gi < lat.num_grids; ++gi) {
-            d.gw[gi] = lat.grids[gi].width;
-            d.gh[gi] = lat.grids[gi].height;
+            // Block records: the logged rectangles count mip-0 blocks.
+            const int w = lat.grids[gi].width, h = lat.grids[gi].height;
+            d.gw[gi] = blocks ? std::max(w >> 2, 1) : w;
+            d.gh[gi] = blocks ? std::max(h >> 2, 1) : h;
         }
     }
     return NT_OK;

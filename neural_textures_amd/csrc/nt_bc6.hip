@@ -297,6 +297,25 @@ __global__ __launch_bounds__(256) void bc6_expand_kernel(Bc6PhaseDesc d)
 template <int C>
 __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
 {
+    // NT_LATENT_TOUCHED: one thread logs the step (the protocol of the fused kernel's texel
+    // log) and, for the first step since the optimizer ran, its block rectangles.
+    if (d.log && blockIdx.x == 0 && threadIdx.x == 0) {
+        UpdateLog *log = d.log;
+        if (log->magic != kUpdateLogMagic) {
+            log->magic = kUpdateLogMagic;
+            log->count = log->consumed = 0u;
+        } else if (log->consumed == log->count) {
+            log->count = log->consumed = 0u;
+        }
+        const uint32_t count = log->count + (log->count < 0xffffffffu ? 1u : 0u);
+        log->count = count;
+        if (count == 1u) {
+            log->kind = kUpdateLogBlocks;
+            for (int gi = 0; gi < NT_MAX_GRIDS; ++gi)
+                for (int k = 0; k < 4; ++k)
+                    log->rect[gi][k] = d.rect[gi][k];
+        }
+    }
     const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (b >= d.total_blocks)
         return;

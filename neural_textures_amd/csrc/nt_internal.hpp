@@ -161,8 +161,12 @@ struct UpdateLog {
     uint64_t magic;
     uint32_t count;    // train steps logged (saturating)
     uint32_t consumed; // count the last optimizer call consumed
+    uint32_t kind;     // what the rectangles count: kUpdateLogTexels or kUpdateLogBlocks
+    uint32_t pad;
     int32_t rect[NT_MAX_GRIDS][4];
 };
+constexpr uint32_t kUpdateLogTexels = 0; // mip-0 texels of unconstrained latents
+constexpr uint32_t kUpdateLogBlocks = 1; // mip-0 blocks of BC6 block records (the BC6 phase's fold)
 constexpr uint64_t kUpdateLogMagic = 0x4554414450555445ull;
 constexpr size_t kUpdateLogBytes = 256;
 constexpr uint32_t kUpdateLogDense = 0x7fffffffu; // a step without rectangles: update every texel
@@ -244,6 +248,10 @@ struct Bc6PhaseDesc {
     Bc6PhaseGrid grid[NT_MAX_GRIDS];
     int G, C;
     int64_t total_blocks;
+    // NT_LATENT_TOUCHED: the update log, in which the fold records each grid's block
+    // rectangle {bx0, bx1, by0, by1} (inclusive, before wrapping); NULL: none.
+    struct UpdateLog *log;
+    int32_t rect[NT_MAX_GRIDS][4];
 };
 
 // Second pass of the two-pass decode, LDS-staged: a workgroup decodes blocks of
@@ -335,8 +343,8 @@ struct LatentAdamDesc {
     float *w[NT_MAX_GRIDS], *g[NT_MAX_GRIDS], *m1[NT_MAX_GRIDS], *m2[NT_MAX_GRIDS];
     int64_t n[NT_MAX_GRIDS]; // floats (unconstrained) or blocks (block records)
     int rec;                 // block record floats (4C+16); 0 = unconstrained
-    // NT_LATENT_TOUCHED (unconstrained, 16 channels): the update log, and each grid's mip-0
-    // size (its chain starts at mip 0).
+    // NT_LATENT_TOUCHED: the update log, and each grid's mip-0 size (its chain starts at
+    // mip 0) in texels, or in blocks for block records.
     UpdateLog *log;
     int C;
     int gw[NT_MAX_GRIDS], gh[NT_MAX_GRIDS];

@@ -812,10 +812,12 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         }
         const uint32_t count = log->count + (log->count < 0xffffffffu ? 1u : 0u);
         log->count = count;
-        if (count == 1u)
+        if (count == 1u) {
+            log->kind = kUpdateLogTexels;
             for (int gi = 0; gi < NT_MAX_GRIDS; ++gi)
                 for (int k = 0; k < 4; ++k)
                     log->rect[gi][k] = d.rect[gi][k];
+        }
     }
 
     // The fields of the grids this lane's group scatters (grid 2j + g), selected once: a

@@ -563,6 +563,49 @@ def test_latent_touched_update_equals_dense(lib, shape, mode, margins):
         nt.check(lib.nt_set_test_hooks(0, 0))
 
 
+@pytest.mark.parametrize("shape", ["ref16", "ref16f"])
+def test_block_touched_update_equals_dense(lib, shape):
+    """NT_LATENT_TOUCHED with BC6 block records: the BC6 phase's fold logs the mip-0 block
+    rectangle of each grid, and nt_optimize_latents then visits only those records. Fed the
+    same block gradients, it must leave every record, moment and gradient bit-identical to
+    the dense scan of every record of every mip (train.cu:641-679, 805-816): over several
+    steps with moving regions (one wrapping past the image edge), from a workspace of random
+    bytes, and with two train steps accumulated before one optimizer call."""
+    import torch
+    say(f"case: touched block Adam {shape}")
+    st = make_state(shape, image=128, region=(64, 32), seed=8, offset=(0, 0), step=1, blocks=True)
+    st.latent_update = abi.NT_LATENT_TOUCHED
+    a = gpu_workspace(lib, st.to_torch(), abi.NT_BLOCK_FEATURES)
+    a.latent_update = abi.NT_LATENT_TOUCHED
+    a.workspace.random_(0, 256)  # a fresh workspace: no valid log
+    b = st.to_torch()
+    b.latent_update = abi.NT_LATENT_DENSE
+    offs = [(3, 5), (100, 110), (40, 17), (64, 96)]
+    for i in range(4):
+        for s in (a, b):
+            s.texel_offset_x, s.texel_offset_y = offs[i]
+            s.step = 1 + i
+        nt.check(lib.nt_train_step(C.byref(a.params()), abi.NT_BLOCK_FEATURES, None))
+        if i == 2:  # two steps accumulate before this optimizer call
+            a.texel_offset_x, a.texel_offset_y = offs[i][1], offs[i][0]
+            nt.check(lib.nt_train_step(C.byref(a.params()), abi.NT_BLOCK_FEATURES, None))
+        sync()
+        for ga, gb in zip(a.grids, b.grids):
+            gb.block_grads.copy_(ga.block_grads)
+        assert any(torch.count_nonzero(g.block_grads) > 0 for g in a.grids)
+        nt.check(lib.nt_optimize_latents(C.byref(a.params()), abi.NT_BLOCK_FEATURES, None))
+        nt.check(lib.nt_optimize_latents(C.byref(b.params()), abi.NT_BLOCK_FEATURES, None))
+        sync()
+        for gi, (ga, gb) in enumerate(zip(a.grids, b.grids)):
+            for name in ("block_params", "block_moment1", "block_moment2", "block_grads"):
+                x, y = getattr(ga, name), getattr(gb, name)
+                assert torch.equal(x.view(torch.int32), y.view(torch.int32)), f"step {i} grid {gi} {name}"
+            assert torch.count_nonzero(ga.block_moment1) > 0
+        for s in (a, b):  # the network gradients are not under test: clear them
+            for arr in (*s.net.weight_grads, *s.net.bias_grads):
+                arr.zero_()
+
+
 # ---- the reference-target pipeline: packing, loss weights, target mips ------------------------------
 
 def _texture_chain(image, nch, rng, mips, weight=1.0):
