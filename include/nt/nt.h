@@ -303,9 +303,9 @@ int nt_optimize_latents(const nt_params *params, nt_kernel_type type, void *stre
 /* One iteration of the reference's training loop body (main.cpp:1071-1076, the calls
  * InvokeTraining, InvokeOptimizeNetwork, InvokeOptimizeFeatures): the same as nt_train_step,
  * nt_optimize_network and nt_optimize_latents called in that order, bit for bit. With
- * NT_UNCONSTRAINED the MLP-gradient reduction and both optimizers share one launch after
- * the train kernel (two launches fewer per iteration); other kernel types make the three
- * calls. Every argument of all three is checked before anything is enqueued. */
+ * every kernel type the MLP-gradient reduction and both optimizers (latent texels or block
+ * records) share one launch after the train step (two launches fewer per iteration). Every
+ * argument of all three is checked before anything is enqueued. */
 int nt_train_iteration(const nt_params *params, nt_kernel_type type, void *stream);
 
 /* Full-image inference at texel centres, mip 0 (InvokeInference, train.cu:1050-1062 ->

@@ -341,6 +341,8 @@ __global__ __launch_bounds__(256) void latent_adam_kernel(LatentAdamDesc d)
 // reduce_rows sums them (kReduceRanges contiguous ranges, each in row order, then the range
 // sums in range order), each of the four thread groups taking four consecutive ranges with
 // all of their loads issued at once.
+__device__ void block_adam_body(const LatentAdamDesc &d, int bid, int nb, int tid);
+
 constexpr int kOptCols = 64, kOptGroups = 4, kOptUnroll = 16;
 constexpr int kOptRangesPerGroup = kReduceRanges / kOptGroups;
 static_assert(kOptRangesPerGroup * kOptGroups == kReduceRanges, "ranges split evenly over the groups");
@@ -348,7 +350,10 @@ static_assert(kOptRangesPerGroup * kOptGroups == kReduceRanges, "ranges split ev
 __global__ __launch_bounds__(kOptCols *kOptGroups) void optimize_step_kernel(OptimizeStepDesc d)
 {
     if ((int)blockIdx.x >= d.nred) {
-        latent_adam_body(d.lat, (int)blockIdx.x - d.nred, (int)gridDim.x - d.nred, threadIdx.x);
+        if (d.lat.rec > 0)
+            block_adam_body(d.lat, (int)blockIdx.x - d.nred, (int)gridDim.x - d.nred, threadIdx.x);
+        else
+            latent_adam_body(d.lat, (int)blockIdx.x - d.nred, (int)gridDim.x - d.nred, threadIdx.x);
         return;
     }
     const ReduceDesc &r = d.red;
@@ -454,22 +459,24 @@ hipError_t launch_optimize_step(const OptimizeStepDesc &d0, hipStream_t s)
     OptimizeStepDesc d = d0;
     d.nred = (d.red.P + kOptCols - 1) / kOptCols;
     const int64_t n = d.lat.start[d.lat.nseg];
-    int64_t lat = (n + kAdamSpan - 1) / kAdamSpan;
+    // Block records: 256 records per workgroup pass (block_adam_body); texels: kAdamSpan.
+    int64_t lat = d.lat.rec > 0 ? (n + 255) / 256 : (n + kAdamSpan - 1) / kAdamSpan;
     if (lat > 8192)
         lat = 8192;
     hipLaunchKernelGGL(optimize_step_kernel, dim3((unsigned)(d.nred + lat)), dim3(kOptCols * kOptGroups), 0, s, d);
     return hipGetLastError();
 }
 
-// Lazy Adam of one float of a block record: `e` of the gradient record at g (rec floats)
-// and of the parameter record at w (rec + 2 floats).
+// Lazy Adam of one float of a block record, its gradient, moments and value loaded at once
+// (in the logged rectangles nearly every gradient is non-zero).
 __device__ __forceinline__ void block_adam_float(const LatentAdamDesc &d, float *w, float *g, float *m1, float *m2)
 {
     const float gs = *g;
+    float a1 = *m1, a2 = *m2;
+    const float wv = *w;
     if (gs == 0.f)
         return;
-    float a1 = *m1, a2 = *m2;
-    *w = adam_update(a1, a2, gs, d.a, *w);
+    *w = adam_update(a1, a2, gs, d.a, wv);
     *m1 = a1;
     *m2 = a2;
     *g = 0.f;
@@ -480,7 +487,7 @@ __device__ __forceinline__ void block_adam_float(const LatentAdamDesc &d, float 
 // log of exactly one BC6-phase train step, only the mip-0 blocks of the logged rectangles
 // are visited (every other record holds zero gradients, which the lazy rule skips), the
 // rectangles' records one after another, each in consecutive floats.
-__global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
+__device__ void block_adam_body(const LatentAdamDesc &d, int bid, int nb, int tid)
 {
     if (d.log) {
         const UpdateLog *log = d.log;
@@ -501,7 +508,7 @@ __global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
                 start[s + 1] = start[s] + (on ? (int64_t)(r[s][1] - r[s][0] + 1) * (r[s][3] - r[s][2] + 1) * rec : 0);
             }
             const int64_t total = start[NT_MAX_GRIDS];
-            for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+            for (int64_t i = (int64_t)bid * 256 + tid; i < total; i += (int64_t)nb * 256) {
                 int s = 0;
 #pragma unroll
                 for (int q = 1; q < NT_MAX_GRIDS; ++q)
@@ -517,7 +524,7 @@ __global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
                                  d.m2[s] + blk * rec + e);
             }
         }
-        if (valid && blockIdx.x == 0 && threadIdx.x == 0)
+        if (valid && bid == 0 && tid == 0)
             d.log->consumed = count;
         if (rects)
             return;
@@ -527,7 +534,7 @@ __global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
     // array read and written in consecutive floats.
     const int64_t total = d.start[d.nseg];
     const int rec = d.rec;
-    for (int64_t r0 = (int64_t)blockIdx.x * 256; r0 < total; r0 += (int64_t)gridDim.x * 256) {
+    for (int64_t r0 = (int64_t)bid * 256; r0 < total; r0 += (int64_t)nb * 256) {
         const int s = adam_segment(d, r0);
         const int64_t b0 = r0 - d.start[s];
         const int64_t left = d.n[s] - b0;
@@ -538,7 +545,7 @@ __global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
         float *g = d.g[s] + b0 * rec;
         float *m1 = d.m1[s] + b0 * rec;
         float *m2 = d.m2[s] + b0 * rec;
-        for (int e = threadIdx.x; e < ne; e += 256) {
+        for (int e = tid; e < ne; e += 256) {
             const float gs = g[e];
             if (gs == 0.f)
                 continue;
@@ -551,6 +558,11 @@ __global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
             g[e] = 0.f;
         }
     }
+}
+
+__global__ __launch_bounds__(256) void block_adam_kernel(LatentAdamDesc d)
+{
+    block_adam_body(d, blockIdx.x, gridDim.x, threadIdx.x);
 }
 
 hipError_t launch_net_adam(const NetAdamDesc &d, hipStream_t s)

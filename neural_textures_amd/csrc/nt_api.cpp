@@ -647,9 +647,9 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     int st = check_mlp(&p->mlp, true, false, &shape);
     if (st)
         return st;
-    if (shape != kShapeRef && shape != kShapeC2 && shape != kShapeC4)
-        return fail(NT_ERR_UNSUPPORTED, "training is built for 12->32->32->16 (C=3), 32->64->64->16 "
-                                        "(C=16) and 64->64->64->64->16 (C=16)");
+    if (shape != kShapeRef && shape != kShapeC1 && shape != kShapeC2 && shape != kShapeC4)
+        return fail(NT_ERR_UNSUPPORTED, "training is built for 12->32->32->16 (C=3), 8->64->64->16 (C=8), "
+                                        "32->64->64->16 (C=16) and 64->64->64->64->16 (C=16)");
     st = check_latents(&p->latents, shape, type != NT_FINALIZE, type != NT_UNCONSTRAINED);
     if (st)
         return st;
@@ -1301,10 +1301,10 @@ int nt_optimize_latents(const nt_params *p, nt_kernel_type type, void *stream)
 }
 
 // One iteration of the reference's loop body (main.cpp:1071-1076): nt_train_step, then
-// nt_optimize_network, then nt_optimize_latents, with the same results. For unconstrained
-// latents the MLP-gradient reduction, the network update and the latent update share one
-// launch after the train kernel; other kernel types make the three calls. Every argument
-// of all three is checked before anything is enqueued.
+// nt_optimize_network, then nt_optimize_latents, with the same results. The MLP-gradient
+// reduction, the network update and the latent update (texels or block records) share one
+// launch after the train step. Every argument of all three is checked before anything is
+// enqueued.
 int nt_train_iteration(const nt_params *p, nt_kernel_type type, void *stream)
 {
     TrainPlan plan;
@@ -1336,15 +1336,6 @@ int nt_train_iteration(const nt_params *p, nt_kernel_type type, void *stream)
         o.net.m2[l] = net.m2[l];
         o.net.bm1[l] = net.bm1[l];
         o.net.bm2[l] = net.bm2[l];
-    }
-    if (type != NT_UNCONSTRAINED) {
-        st = nt_train_step(p, type, stream);
-        if (st)
-            return st;
-        st = hip_status(launch_net_adam(net, (hipStream_t)stream), "network Adam launch");
-        if (st)
-            return st;
-        return hip_status(launch_latent_adam(o.lat, (hipStream_t)stream), "latent Adam launch");
     }
     st = train_step_with(p, type, stream, plan, (uint8_t *)p->workspace, update_log(p), &o.red);
     if (st)

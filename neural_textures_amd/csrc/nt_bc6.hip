@@ -252,10 +252,41 @@ __device__ __forceinline__ int wrap_mod(int v, int n)
     return r < 0 ? r + n : r;
 }
 
+// A block record's fields a pixel thread needs, all loads issued at once (the partition
+// picks the endpoints afterwards): the four endpoints of every channel, the pixel's index
+// on the segment, the partition and the mode.
+template <int C>
+struct Bc6Pixel {
+    float q0[C], q1[C]; // the pixel's partition's endpoints, unquantized
+    float xi;
+    int part, bits;
+};
+template <int C>
+__device__ __forceinline__ Bc6Pixel<C> bc6_pixel(const float *rec, int pix)
+{
+    float e[4][C];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch)
+            e[k][ch] = rec[k * C + ch];
+    Bc6Pixel<C> q;
+    q.xi = rec[4 * C + pix];
+    const int partition = __float_as_int(rec[4 * C + 16]);
+    q.bits = bc6_mode_bits(__float_as_int(rec[4 * C + 17]));
+    q.part = (bc6_partition_mask(partition) >> pix) & 1;
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) {
+        q.q0[ch] = bc6_unquantize(q.part ? e[2][ch] : e[0][ch], q.bits);
+        q.q1[ch] = bc6_unquantize(q.part ? e[3][ch] : e[1][ch], q.bits);
+    }
+    return q;
+}
+
 // Expansion: one thread per texel of a block rectangle, numbered block by block and, in a
 // block, row-major, so that 16 consecutive threads share one record. Each texel's C values are the
 // reference's BC6 decode of its block (train.cu:240-261, DecompressBC6 :169-182), the same
-// function the per-sample gather applies; its gradients are cleared.
+// arithmetic as the per-sample gather (bc6_decompress); its gradients are cleared.
 template <int C>
 __global__ __launch_bounds__(256) void bc6_expand_kernel(Bc6PhaseDesc d)
 {
@@ -264,27 +295,27 @@ __global__ __launch_bounds__(256) void bc6_expand_kernel(Bc6PhaseDesc d)
     if (b >= d.total_blocks)
         return;
     const Bc6PhaseGrid &g = d.grid[bc6_phase_grid(d, b)];
-    const int64_t lb = b - g.first_block;
-    const int bx = wrap_mod(g.bx0 + (int)(lb % g.nbx), g.nbu);
-    const int by = wrap_mod(g.by0 + (int)(lb / g.nbx), g.nbv);
+    // A grid's rectangle holds fewer than 2^31 blocks (its blocks fit 32-bit offsets).
+    const int lb = (int)(b - g.first_block);
+    const int ry = lb / g.nbx;
+    const int bx = wrap_mod(g.bx0 + (lb - ry * g.nbx), g.nbu);
+    const int by = wrap_mod(g.by0 + ry, g.nbv);
     const int pix = (int)(t & 15);
-    const float *rec = g.params + ((int64_t)by * g.nbu + bx) * (4 * C + 18);
-    const int partition = __float_as_int(rec[4 * C + 16]);
-    const int bits = bc6_mode_bits(__float_as_int(rec[4 * C + 17]));
-    const int part = (bc6_partition_mask(partition) >> pix) & 1;
-    const float xi = rec[4 * C + pix];
+    const Bc6Pixel<C> q = bc6_pixel<C>(g.params + ((int64_t)by * g.nbu + bx) * (4 * C + 18), pix);
     const int x = 4 * bx + (pix & 3), y = 4 * by + (pix >> 2);
     const int64_t o = ((int64_t)y * g.w + x) * C;
 #pragma unroll
     for (int ch = 0; ch < C; ++ch) {
-        g.values[o + ch] = bc6_decompress(rec[2 * part * C + ch], rec[(2 * part + 1) * C + ch], bits, xi);
+        const float yv = bc6_y(q.q0[ch], q.q1[ch], q.xi);
+        const int hy = bc6_hy(yv);
+        g.values[o + ch] = ldexpf(yv / 1024.f - (float)hy, hy - 14);
         g.tgrads[o + ch] = 0.f;
     }
 }
 
-// Fold: one thread per block of the rectangle. The reference adds, for every corner that
-// lands on texel (pixel p) of a block, with feature gradient w * g per channel
-// (train.cu:405-455):
+// Fold: one thread per texel of the block rectangle, as the expansion. The reference adds,
+// for every corner that lands on texel (pixel p) of a block, with feature gradient w * g per
+// channel (train.cu:405-455):
 //   dl_dy = ldexp(w g, hy - 24),   hy from y = q0 + 8 (q1 - q0) x_p  (that texel's channel)
 //   pixel index p:    += sum_ch dl_dy * 8 (q1 - q0)
 //   endpoints of p's partition, channel ch:  e0 += (1 - 8 x_p) (31/64) 2^(16 - bits) dl_dy,
@@ -292,8 +323,10 @@ __global__ __launch_bounds__(256) void bc6_expand_kernel(Bc6PhaseDesc d)
 // Every factor but w g depends on the texel and channel only, and ldexp by an integer is
 // exact, so the sums over corners equal these terms applied to the texel's gradient
 // G = sum w g (which the fused kernel accumulated) up to the order of the fp32 additions
-// (which the reference's atomics leave open as well). Texels with a zero gradient add
-// nothing; the block's record gradients are read, added to and written by this thread only.
+// (which the reference's atomics leave open as well). The pixel thread adds its pixel-index
+// gradient; the endpoint terms are summed over the block's 16 threads with lane shuffles
+// and added by its first thread. Texels with a zero gradient add nothing; each record field
+// is read, added to and written by one thread only.
 template <int C>
 __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
 {
@@ -316,81 +349,68 @@ __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
                     log->rect[gi][k] = d.rect[gi][k];
         }
     }
-    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    // The 16 threads of a block are 16 consecutive lanes of one wave (the launch covers
+    // whole blocks), so every shuffle below stays within the block's lanes.
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t b = t >> 4;
     if (b >= d.total_blocks)
         return;
     const Bc6PhaseGrid &g = d.grid[bc6_phase_grid(d, b)];
-    const int64_t lb = b - g.first_block;
-    const int bx = wrap_mod(g.bx0 + (int)(lb % g.nbx), g.nbu);
-    const int by = wrap_mod(g.by0 + (int)(lb / g.nbx), g.nbv);
-    float G[16][C];
-    bool any = false;
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-        const int64_t o = ((int64_t)(4 * by + (p >> 2)) * g.w + 4 * bx + (p & 3)) * C;
-#pragma unroll
-        for (int ch = 0; ch < C; ++ch) {
-            G[p][ch] = g.tgrads[o + ch];
-            any |= G[p][ch] != 0.f;
-        }
-    }
-    if (!any)
-        return;
+    // A grid's rectangle holds fewer than 2^31 blocks (its blocks fit 32-bit offsets).
+    const int lb = (int)(b - g.first_block);
+    const int ry = lb / g.nbx;
+    const int bx = wrap_mod(g.bx0 + (lb - ry * g.nbx), g.nbu);
+    const int by = wrap_mod(g.by0 + ry, g.nbv);
+    const int pix = (int)(t & 15);
     const int64_t blk = (int64_t)by * g.nbu + bx;
-    const float *rec = g.params + blk * (4 * C + 18);
+    const int64_t o = ((int64_t)(4 * by + (pix >> 2)) * g.w + 4 * bx + (pix & 3)) * C;
+    float G[C];
+    bool touched = false;
+#pragma unroll
+    for (int ch = 0; ch < C; ++ch) {
+        G[ch] = g.tgrads[o + ch];
+        touched |= G[ch] != 0.f;
+    }
+    // Lanes of the block with a non-zero gradient (the block's 16-bit slice of the wave's).
+    const uint64_t vote = __ballot(touched);
+    const int lane = (int)(threadIdx.x & 63);
+    if (((vote >> (lane & ~15)) & 0xFFFFull) == 0)
+        return; // the whole block untouched (all 16 lanes leave together)
+    const Bc6Pixel<C> q = bc6_pixel<C>(g.params + blk * (4 * C + 18), pix);
     float *grec = g.grads + blk * (4 * C + 16);
-    const int mask = bc6_partition_mask(__float_as_int(rec[4 * C + 16]));
-    const int bits = bc6_mode_bits(__float_as_int(rec[4 * C + 17]));
-    const float deibar = ldexpf(31.f / 64.f, 16 - bits);
-    float q[4][C];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int ch = 0; ch < C; ++ch)
-            q[e][ch] = bc6_unquantize(rec[e * C + ch], bits);
+    const float deibar = ldexpf(31.f / 64.f, 16 - q.bits);
+    const float alpha = ldexpf(q.xi, 3);
+    float dl_dx = 0.f;
     float de[4][C];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int ch = 0; ch < C; ++ch)
-            de[e][ch] = 0.f;
-#pragma unroll
-    for (int p = 0; p < 16; ++p) {
-        bool touched = false;
-#pragma unroll
-        for (int ch = 0; ch < C; ++ch)
-            touched |= G[p][ch] != 0.f;
-        if (!touched)
-            continue;
-        const int part = (mask >> p) & 1;
-        const float xi = rec[4 * C + p];
-        const float alpha = ldexpf(xi, 3);
-        float dl_dx = 0.f;
-#pragma unroll
-        for (int ch = 0; ch < C; ++ch) {
-            const float q0 = part ? q[2][ch] : q[0][ch];
-            const float q1 = part ? q[3][ch] : q[1][ch];
-            const int hy = bc6_hy(bc6_y(q0, q1, xi));
-            const float dl_dy = ldexpf(G[p][ch], hy - 24);
-            dl_dx += dl_dy * ldexpf(q1 - q0, 3);
-            const float a0 = ((1.f - alpha) * deibar) * dl_dy;
-            const float a1 = (alpha * deibar) * dl_dy;
-            if (part) {
-                de[2][ch] += a0;
-                de[3][ch] += a1;
-            } else {
-                de[0][ch] += a0;
-                de[1][ch] += a1;
-            }
-        }
-        grec[4 * C + p] += dl_dx;
+    for (int ch = 0; ch < C; ++ch) {
+        const int hy = bc6_hy(bc6_y(q.q0[ch], q.q1[ch], q.xi));
+        const float dl_dy = ldexpf(G[ch], hy - 24);
+        dl_dx += dl_dy * ldexpf(q.q1[ch] - q.q0[ch], 3);
+        const float a0 = touched ? ((1.f - alpha) * deibar) * dl_dy : 0.f;
+        const float a1 = touched ? (alpha * deibar) * dl_dy : 0.f;
+        de[0][ch] = q.part ? 0.f : a0;
+        de[1][ch] = q.part ? 0.f : a1;
+        de[2][ch] = q.part ? a0 : 0.f;
+        de[3][ch] = q.part ? a1 : 0.f;
     }
+    if (touched)
+        grec[4 * C + pix] += dl_dx;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (int m = 8; m > 0; m >>= 1)
 #pragma unroll
-        for (int ch = 0; ch < C; ++ch)
-            if (de[e][ch] != 0.f)
-                grec[e * C + ch] += de[e][ch];
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int ch = 0; ch < C; ++ch)
+                de[k][ch] += __shfl_xor(de[k][ch], m, 16);
+    if (pix == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int ch = 0; ch < C; ++ch)
+                if (de[k][ch] != 0.f)
+                    grec[k * C + ch] += de[k][ch];
+    }
 }
 
 hipError_t launch_bc6_expand(const Bc6PhaseDesc &d, hipStream_t s)
@@ -410,7 +430,8 @@ hipError_t launch_bc6_fold(const Bc6PhaseDesc &d, hipStream_t s)
         return hipSuccess;
     if (d.C != 3)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(bc6_fold_kernel<3>, dim3((unsigned)((d.total_blocks + 255) / 256)), dim3(256), 0, s, d);
+    hipLaunchKernelGGL(bc6_fold_kernel<3>, dim3((unsigned)((d.total_blocks * 16 + 255) / 256)), dim3(256), 0, s,
+                       d);
     return hipGetLastError();
 }
 

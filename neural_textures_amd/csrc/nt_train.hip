@@ -1233,6 +1233,7 @@ static hipError_t launch_typed(int type, const TrainDesc &d, int num_wg, size_t 
 }
 
 using ShapeRef = Shape<16, 32, 2>;
+using ShapeC1 = Shape<16, 64, 2>; // BASELINE config 1's network: one grid of 8 channels, 8 -> 64 -> 64 -> 3
 using ShapeC2 = Shape<32, 64, 2>;
 using ShapeC4 = Shape<64, 64, 3>;
 
@@ -1241,6 +1242,8 @@ hipError_t launch_train(int shape, int type, const TrainDesc &d, int num_wg, siz
     switch (shape) {
     case kShapeRef:
         return launch_typed<ShapeRef, 3>(type, d, num_wg, lds, s);
+    case kShapeC1:
+        return launch_typed<ShapeC1, 8>(type, d, num_wg, lds, s);
     case kShapeC2:
         return launch_typed<ShapeC2, 16>(type, d, num_wg, lds, s);
     case kShapeC4:
@@ -1255,6 +1258,8 @@ hipError_t launch_prep_weights(int shape, const PrepDesc &d, hipStream_t s)
     switch (shape) {
     case kShapeRef:
         return launch_prep<ShapeRef>(d, s);
+    case kShapeC1:
+        return launch_prep<ShapeC1>(d, s);
     case kShapeC2:
         return launch_prep<ShapeC2>(d, s);
     case kShapeC4:
@@ -1275,6 +1280,8 @@ size_t train_weight_bytes(int shape)
     switch (shape) {
     case kShapeRef:
         return weight_bytes<ShapeRef>();
+    case kShapeC1:
+        return weight_bytes<ShapeC1>();
     case kShapeC2:
         return weight_bytes<ShapeC2>();
     case kShapeC4:
@@ -1289,6 +1296,8 @@ size_t train_frag_bytes(int shape)
     switch (shape) {
     case kShapeRef:
         return (size_t)ShapeRef::all_frags() * kWave * 16;
+    case kShapeC1:
+        return (size_t)ShapeC1::all_frags() * kWave * 16;
     case kShapeC2:
         return (size_t)ShapeC2::all_frags() * kWave * 16;
     case kShapeC4:
@@ -1303,6 +1312,8 @@ size_t train_xt_bytes(int shape)
     switch (shape) {
     case kShapeRef:
         return TrainLayout<ShapeRef>::transpose_bytes;
+    case kShapeC1:
+        return TrainLayout<ShapeC1>::transpose_bytes;
     case kShapeC2:
         return TrainLayout<ShapeC2>::transpose_bytes;
     case kShapeC4:
@@ -1317,6 +1328,8 @@ size_t train_lds_static(int shape)
     switch (shape) {
     case kShapeRef:
         return TrainLayout<ShapeRef>::head_bytes;
+    case kShapeC1:
+        return TrainLayout<ShapeC1>::head_bytes;
     case kShapeC2:
         return TrainLayout<ShapeC2>::head_bytes;
     case kShapeC4:
@@ -1331,6 +1344,8 @@ int train_grad_total(int shape)
     switch (shape) {
     case kShapeRef:
         return ShapeRef::grad_total();
+    case kShapeC1:
+        return ShapeC1::grad_total();
     case kShapeC2:
         return ShapeC2::grad_total();
     case kShapeC4:

@@ -32,6 +32,10 @@ SHAPES = {
     # ... and as BCf-1k: only the finest grid leaves the MFMA reduction, the others keep it
     "ref16h": dict(sizes=[12, 32, 32, 16], C=3, grids=[(0.5, 4), (0.25, 4), (0.125, 3), (0.0625, 3)],
                    tex=[3, 3, 3]),
+    # BASELINE config 1's network: one grid of 8 channels, 8 -> 64 -> 64 -> 3 (half and full
+    # the image's size)
+    "c1": dict(sizes=[8, 64, 64, 3], C=8, grids=[(0.5, 3)], tex=[3]),
+    "c1f": dict(sizes=[8, 64, 64, 3], C=8, grids=[(1.0, 3)], tex=[3]),
     # 2 grids x 16 channels, 32 -> 64 -> 64 -> 9
     "c2": dict(sizes=[32, 64, 64, 9], C=16, grids=[(0.25, 3), (0.125, 3)], tex=[3, 3, 3]),
     # BASELINE configs 4/5: 4 grids x 16 channels, 64 -> 64 -> 64 -> 64 -> 12

@@ -143,6 +143,11 @@ TRAIN_CASES = [
     ("ref16ff", 128, (64, 48), (100, 110), abi.NT_UNCONSTRAINED),
     ("ref16h", 128, (64, 32), (40, 9), abi.NT_UNCONSTRAINED),
     ("ref16h", 128, (64, 48), (100, 110), abi.NT_UNCONSTRAINED),
+    # BASELINE config 1's network (8 -> 64 -> 64 -> 3, one 8-channel grid) on the general kernel
+    ("c1", 128, (64, 32), (16, 40), abi.NT_UNCONSTRAINED),
+    ("c1", 64, (50, 21), (3, 5), abi.NT_UNCONSTRAINED),          # ragged region and tail row
+    ("c1f", 128, (64, 48), (100, 90), abi.NT_UNCONSTRAINED),     # wraps; a grid as fine as the image
+    ("c1", 128, (64, 32), (0, 0), abi.NT_BLOCK_FEATURES),
     ("c2", 128, (64, 32), (16, 40), abi.NT_UNCONSTRAINED),
     ("c2", 64, (50, 21), (3, 5), abi.NT_UNCONSTRAINED),         # ragged region and tail row
     ("c2", 128, (64, 48), (100, 90), abi.NT_UNCONSTRAINED),     # wraps: clamped edge samples
@@ -246,9 +251,9 @@ def test_train_step_scatter_out_of_box_paths(lib, O, shape):
     check_train_grads(st, gs, alt, biases=False)
 
 
-@pytest.mark.parametrize("shape,region,max_wg", [("ref", (64, 32), 0), ("c2", (64, 32), 0), ("c4", (64, 32), 0),
-                                                 ("c2", (50, 13), 2), ("c4", (100, 7), 1)],
-                         ids=["ref", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg"])
+@pytest.mark.parametrize("shape,region,max_wg", [("ref", (64, 32), 0), ("c1", (64, 32), 0), ("c2", (64, 32), 0),
+                                                 ("c4", (64, 32), 0), ("c2", (50, 13), 2), ("c4", (100, 7), 1)],
+                         ids=["ref", "c1", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg"])
 def test_train_step_random_texels(lib, O, shape, region, max_wg):
     """NT_SAMPLES_RANDOM: samples anywhere in the image (the 16-channel kernel with taps
     from global memory and per-sample corner atomics; the general kernel for the reference
