@@ -297,29 +297,29 @@ UpdateLog *update_log(const nt_params *p)
 // Texel rectangle {x0, x1, y0, y1} of grid g (inclusive, before wrapping: x0 and y0 may
 // be negative, x1 and y1 past the grid) that holds every bilinear corner a train step's
 // positions reach; the whole grid where the positions are random or span it.
-void footprint_rect(const nt_params *p, const nt_grid &g, int (&rect)[4])
+void footprint_rect(const nt_params *p, int width, int height, int (&rect)[4])
 {
     if (p->sample_mode == NT_SAMPLES_RANDOM) {
         rect[0] = rect[2] = 0;
-        rect[1] = g.width - 1;
-        rect[3] = g.height - 1;
+        rect[1] = width - 1;
+        rect[3] = height - 1;
         return;
     }
     // Positions lie in [off, off + extent] texels of the image (jitter and clamping
     // included); their footprints' corners at floor(pos * r - 0.5) + {0, 1}, with a texel
     // of margin on each side for rounding.
     const int rw = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
-    const double rx = (double)g.width / p->image_width, ry = (double)g.height / p->image_height;
+    const double rx = (double)width / p->image_width, ry = (double)height / p->image_height;
     const int rows = (int)(((int64_t)p->num_samples + rw - 1) / rw);
     const int x0 = (int)std::floor(p->texel_offset_x * rx - 0.5) - 1;
     const int x1 = (int)std::floor((double)(p->texel_offset_x + rw) * rx - 0.5) + 2;
     const int y0 = (int)std::floor(p->texel_offset_y * ry - 0.5) - 1;
     const int y1 = (int)std::floor((double)(p->texel_offset_y + rows) * ry - 0.5) + 2;
     // Wider than the grid: the whole width (height) of it.
-    rect[0] = x1 - x0 + 1 >= g.width ? 0 : x0;
-    rect[1] = x1 - x0 + 1 >= g.width ? g.width - 1 : x1;
-    rect[2] = y1 - y0 + 1 >= g.height ? 0 : y0;
-    rect[3] = y1 - y0 + 1 >= g.height ? g.height - 1 : y1;
+    rect[0] = x1 - x0 + 1 >= width ? 0 : x0;
+    rect[1] = x1 - x0 + 1 >= width ? width - 1 : x1;
+    rect[2] = y1 - y0 + 1 >= height ? 0 : y0;
+    rect[3] = y1 - y0 + 1 >= height ? height - 1 : y1;
 }
 
 struct TrainPlan {
@@ -333,11 +333,15 @@ struct TrainPlan {
     // The 16-channel unconstrained kernel (nt_train16.hip), when it applies.
     int use16, groups, rows;
     Train16Desc t16;
-    // The BC6 block phase on that kernel (Bc6PhaseDesc): block rectangles, and the
-    // workspace offsets of each grid's expanded texels and their gradients.
+    // The BC6 block phase (Bc6PhaseDesc): the rest of the plan is the inner unconstrained
+    // step's. Per grid the mips the inner step sees (its chain stops after the last level a
+    // sample reaches) and the workspace offsets of the expanded chain and its gradients; per
+    // level its grid and mip.
     int bc6;
     Bc6PhaseDesc bc6d;
+    int bc6_mips[NT_MAX_GRIDS];
     size_t bc6_values_off[NT_MAX_GRIDS], bc6_grads_off[NT_MAX_GRIDS];
+    int bc6_level_grid[2 * NT_MAX_GRIDS], bc6_level_mip[2 * NT_MAX_GRIDS];
 };
 
 constexpr size_t kMaxLds = 160 * 1024;
@@ -570,48 +574,108 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
 
 int floor_div4(int v) { return v >= 0 ? v / 4 : -((3 - v) / 4); }
 
-// The BC6 block phase (NT_BLOCK_FEATURES, NT_FINALIZE) of the reference network with region
-// sampling runs the fused unconstrained kernel on texels expanded from the block records
-// (Bc6PhaseDesc): the kernel is planned for the same step with 1-mip grids of the same
-// sizes whose texels live in the workspace, after its own partial rows. Sets plan->bc6.
+// Texel offset of mip m in a dense chain of a width x height grid (nt_mip_chain_layout).
+int64_t chain_offset(int width, int height, int m)
+{
+    int64_t o = 0;
+    for (int k = 0; k < m; ++k)
+        o += (int64_t)mip_dim_h(width, k) * mip_dim_h(height, k);
+    return o;
+}
+
+// The mips a step with mip coordinate z samples in a chain of num_mips (train.cu:266-281):
+// floor(z) and, when z has a fraction, floor(z) + 1, both clamped to the last mip.
+int mip_pair(int num_mips, float z, int (&m)[2])
+{
+    const float zb = floorf(z);
+    const int top = num_mips - 1;
+    m[0] = std::min((int)std::min(zb, (float)top), top);
+    m[1] = std::min(m[0] + 1, top);
+    return z - zb > 0.f ? 2 : 1;
+}
+
+// The inner unconstrained step of the BC6 phase: p with every grid's values and gradients
+// replaced by the expanded chain in the workspace at ws (stand-in addresses, 256-byte
+// aligned like the real ones, when ws is NULL), mips up to the last level sampled.
+nt_params bc6_inner(const nt_params *p, const TrainPlan &plan, uint8_t *ws)
+{
+    nt_params q = *p;
+    q.latent_update = NT_LATENT_DENSE;
+    for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+        nt_grid &g = q.latents.grids[gi];
+        g.num_mips = plan.bc6_mips[gi];
+        for (int m = 0; m < NT_MAX_MIPS; ++m)
+            g.mip_offset[m] = m < g.num_mips ? chain_offset(g.width, g.height, m) : 0;
+        g.values = ws ? (float *)(ws + plan.bc6_values_off[gi]) : (float *)(uintptr_t)256;
+        g.grads = ws ? (float *)(ws + plan.bc6_grads_off[gi]) : (float *)(uintptr_t)256;
+    }
+    return q;
+}
+
+int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan);
+
+// The BC6 block phase (NT_BLOCK_FEATURES, NT_FINALIZE) runs an unconstrained train step on
+// texels expanded from the block records of every level a sample reaches (Bc6PhaseDesc):
+// the step is planned as one over grids whose texels live in the workspace, after its own
+// scratch. Sets plan->bc6 (and then the inner step's plan), or leaves the plan alone.
 void plan_bc6_phase(const nt_params *p, TrainPlan *plan)
 {
     plan->bc6 = 0;
-    if (plan->shape != kShapeRef || p->sample_mode != NT_SAMPLES_REGION || p->sample_mip != 0.f)
-        return;
     const int C = p->latents.channels, G = p->latents.num_grids;
-    nt_params q = *p;
-    q.latent_update = NT_LATENT_DENSE;
-    for (int gi = 0; gi < G; ++gi) {
-        nt_grid &g = q.latents.grids[gi];
-        // Whole blocks only: the expansion and the fold address texels block by block.
-        if ((g.width & 3) || (g.height & 3))
-            return;
-        g.num_mips = 1;
-        g.mip_offset[0] = 0;
-        // Stand-ins for the workspace arrays (set at launch); 256-byte aligned like them.
-        g.values = g.grads = (float *)(uintptr_t)256;
-    }
-    TrainPlan t = *plan;
-    plan16(&q, NT_UNCONSTRAINED, &t);
-    if (!t.use16)
+    if (C != 3 && C != 8 && C != 16)
         return;
-    *plan = t;
-    Bc6PhaseDesc &b = plan->bc6d;
-    b = Bc6PhaseDesc{};
-    b.G = G;
-    b.C = C;
-    size_t off = (plan->workspace + 255) & ~(size_t)255;
-    int64_t first = 0;
+    TrainPlan t = *plan;
+    t.bc6 = 0;
+    int levels = 0;
     for (int gi = 0; gi < G; ++gi) {
         const nt_grid &g = p->latents.grids[gi];
-        Bc6PhaseGrid &x = b.grid[gi];
-        x.w = g.width;
-        x.h = g.height;
-        x.nbu = g.width / 4;
-        x.nbv = g.height / 4;
+        int m[2];
+        const int n = mip_pair(g.num_mips, p->sample_mip, m);
+        t.bc6_mips[gi] = (n == 2 ? m[1] : m[0]) + 1;
+        for (int k = 0; k < n; ++k) {
+            if (k == 1 && m[1] == m[0])
+                break; // both weights on the last mip: one level
+            t.bc6_level_grid[levels] = gi;
+            t.bc6_level_mip[levels] = m[k];
+            ++levels;
+        }
+    }
+    const nt_params q = bc6_inner(p, t, nullptr);
+    TrainPlan inner;
+    if (plan_train(&q, NT_UNCONSTRAINED, &inner) != NT_OK)
+        return;
+    // The inner plan, with the phase's fields.
+    for (int gi = 0; gi < G; ++gi)
+        inner.bc6_mips[gi] = t.bc6_mips[gi];
+    for (int k = 0; k < levels; ++k) {
+        inner.bc6_level_grid[k] = t.bc6_level_grid[k];
+        inner.bc6_level_mip[k] = t.bc6_level_mip[k];
+    }
+    Bc6PhaseDesc &b = inner.bc6d;
+    b = Bc6PhaseDesc{};
+    b.nlevels = levels;
+    b.C = C;
+    size_t off = (inner.workspace + 255) & ~(size_t)255;
+    for (int gi = 0; gi < G; ++gi) {
+        const nt_grid &g = p->latents.grids[gi];
+        const size_t bytes =
+            ((size_t)chain_offset(g.width, g.height, inner.bc6_mips[gi]) * C * sizeof(float) + 255) & ~(size_t)255;
+        inner.bc6_values_off[gi] = off;
+        off += bytes;
+        inner.bc6_grads_off[gi] = off;
+        off += bytes;
+    }
+    int64_t first = 0;
+    for (int k = 0; k < levels; ++k) {
+        const nt_grid &g = p->latents.grids[inner.bc6_level_grid[k]];
+        const int m = inner.bc6_level_mip[k];
+        Bc6PhaseLevel &x = b.level[k];
+        x.w = mip_dim_h(g.width, m);
+        x.h = mip_dim_h(g.height, m);
+        x.nbu = std::max(x.w >> 2, 1);
+        x.nbv = std::max(x.h >> 2, 1);
         int r[4];
-        footprint_rect(p, g, r);
+        footprint_rect(p, x.w, x.h, r);
         x.bx0 = floor_div4(r[0]);
         x.nbx = floor_div4(r[1]) - x.bx0 + 1;
         if (x.nbx >= x.nbu) {
@@ -626,15 +690,11 @@ void plan_bc6_phase(const nt_params *p, TrainPlan *plan)
         }
         x.first_block = first;
         first += (int64_t)x.nbx * x.nby;
-        const size_t bytes = ((size_t)g.width * g.height * C * sizeof(float) + 255) & ~(size_t)255;
-        plan->bc6_values_off[gi] = off;
-        off += bytes;
-        plan->bc6_grads_off[gi] = off;
-        off += bytes;
     }
     b.total_blocks = first;
-    plan->workspace = off;
-    plan->bc6 = 1;
+    inner.workspace = off;
+    inner.bc6 = 1;
+    *plan = inner;
 }
 
 int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
@@ -666,8 +726,6 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         return fail(NT_ERR_INVALID_ARGUMENT, "latent_update %d", p->latent_update);
     if (!std::isfinite(p->sample_mip) || p->sample_mip < 0.f)
         return fail(NT_ERR_INVALID_ARGUMENT, "sample_mip %g", (double)p->sample_mip);
-    if (p->sample_mip != 0.f && type != NT_UNCONSTRAINED)
-        return fail(NT_ERR_UNSUPPORTED, "sample_mip > 0 is built for unconstrained latents only");
     const int rw = p->region_width > 0 ? p->region_width : NT_DEFAULT_REGION;
     const int rows = (int)(((int64_t)p->num_samples + rw - 1) / rw);
     plan->shape = shape;
@@ -768,8 +826,11 @@ int plan_train(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->rows = plan->nwg;
     plan->bc6 = 0;
     plan16(p, type, plan);
-    if (type != NT_UNCONSTRAINED && !plan->use16)
+    if (type != NT_UNCONSTRAINED)
         plan_bc6_phase(p, plan);
+    if (type != NT_UNCONSTRAINED && !plan->bc6)
+        return fail(NT_ERR_UNSUPPORTED, "block records train through the BC6 phase, built for 3, 8 and 16 "
+                                        "channels");
     return NT_OK;
 }
 
@@ -916,24 +977,28 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
     hipStream_t s = (hipStream_t)stream;
     float *partial = (float *)(ws + plan.weight_bytes);
     hipError_t e;
-    const bool bc6_log = plan.bc6 && type == NT_BLOCK_FEATURES;
-    Bc6PhaseDesc b6{};
     if (plan.bc6) {
-        b6 = plan.bc6d;
+        // The BC6 phase: expand the sampled levels' block records, run the unconstrained
+        // step on the expanded texels, fold their gradients back into the records.
+        Bc6PhaseDesc b6 = plan.bc6d;
         const int C = p->latents.channels;
-        for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+        for (int k = 0; k < b6.nlevels; ++k) {
+            const int gi = plan.bc6_level_grid[k], m = plan.bc6_level_mip[k];
             const nt_grid &g = p->latents.grids[gi];
-            Bc6PhaseGrid &x = b6.grid[gi];
-            x.params = g.block_params + g.block_offset[0] * (4 * C + 18);
-            x.grads = g.block_grads ? g.block_grads + g.block_offset[0] * (4 * C + 16) : nullptr;
-            x.values = (float *)(ws + plan.bc6_values_off[gi]);
-            x.tgrads = (float *)(ws + plan.bc6_grads_off[gi]);
+            Bc6PhaseLevel &x = b6.level[k];
+            const int64_t texel0 = chain_offset(g.width, g.height, m) * C;
+            x.params = g.block_params + g.block_offset[m] * (4 * C + 18);
+            x.grads = g.block_grads ? g.block_grads + g.block_offset[m] * (4 * C + 16) : nullptr;
+            x.values = (float *)(ws + plan.bc6_values_off[gi]) + texel0;
+            x.tgrads = (float *)(ws + plan.bc6_grads_off[gi]) + texel0;
         }
-        // The fold logs the block rectangles (BLOCK_FEATURES; other types log a dense step).
-        b6.log = bc6_log ? log : nullptr;
+        // Samples at z = 0 reach mip 0 only, one level per grid: the fold logs each grid's
+        // block rectangle for NT_LATENT_TOUCHED; otherwise the step logs as dense.
+        const bool rects = type == NT_BLOCK_FEATURES && p->sample_mip == 0.f && b6.nlevels == p->latents.num_grids;
+        b6.log = rects ? log : nullptr;
         for (int gi = 0; gi < NT_MAX_GRIDS; ++gi) {
-            const Bc6PhaseGrid &x = b6.grid[gi];
-            const bool on = gi < p->latents.num_grids;
+            const bool on = rects && gi < b6.nlevels;
+            const Bc6PhaseLevel &x = b6.level[on ? gi : 0];
             b6.rect[gi][0] = on ? x.bx0 : 0;
             b6.rect[gi][1] = on ? x.bx0 + x.nbx - 1 : -1;
             b6.rect[gi][2] = on ? x.by0 : 0;
@@ -942,8 +1007,25 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
         e = launch_bc6_expand(b6, s);
         if (e != hipSuccess)
             return hip_status(e, "BC6 expansion launch");
+        const nt_params q = bc6_inner(p, plan, ws);
+        TrainPlan in = plan;
+        in.bc6 = 0;
+        const int st = train_step_with(&q, NT_UNCONSTRAINED, stream, in, ws, nullptr, deferred);
+        if (st)
+            return st;
+        if (type == NT_BLOCK_FEATURES) {
+            e = launch_bc6_fold(b6, s);
+            if (e != hipSuccess)
+                return hip_status(e, "BC6 fold launch");
+        }
+        if (log && !b6.log) {
+            e = launch_log_dense_step(log, s);
+            if (e != hipSuccess)
+                return hip_status(e, "update log launch");
+        }
+        return ok();
     }
-    if (log && !(plan.use16 && type == NT_UNCONSTRAINED) && !bc6_log) {
+    if (log && !(plan.use16 && type == NT_UNCONSTRAINED)) {
         // This kernel does not record its footprints: the optimizer updates every texel.
         e = launch_log_dense_step(log, s);
         if (e != hipSuccess)
@@ -954,13 +1036,13 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
         d.mlp = mlp_desc(&p->mlp);
         d.partial = partial;
         d.log = log;
-        if (plan.bc6) {
-            // The block phase trains on the expanded texels; the block Adam scans densely.
-            d.log = nullptr;
-            for (int gi = 0; gi < p->latents.num_grids; ++gi) {
-                d.grid[gi].values = b6.grid[gi].values;
-                d.grid[gi].grads = b6.grid[gi].tgrads;
-            }
+        // The grids' arrays come from the params of this call, never from the plan: a plan
+        // may be made before the arrays exist (the BC6 phase plans its inner step over
+        // stand-in addresses for the workspace it has not been given yet).
+        for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+            const nt_grid &g = p->latents.grids[gi];
+            d.grid[gi].values = g.values + g.mip_offset[0] * p->latents.channels;
+            d.grid[gi].grads = g.grads + g.mip_offset[0] * p->latents.channels;
         }
         for (int gi = 0; gi < NT_MAX_GRIDS && d.log; ++gi) {
             if (gi >= p->latents.num_grids) {
@@ -968,7 +1050,7 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
                 d.rect[gi][1] = d.rect[gi][3] = -1;
                 continue;
             }
-            footprint_rect(p, p->latents.grids[gi], d.rect[gi]);
+            footprint_rect(p, p->latents.grids[gi].width, p->latents.grids[gi].height, d.rect[gi]);
         }
         {
             ProfileScope prof(s);
@@ -976,11 +1058,6 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
         }
         if (e != hipSuccess)
             return hip_status(e, "train kernel launch");
-        if (plan.bc6 && type == NT_BLOCK_FEATURES) {
-            e = launch_bc6_fold(b6, s);
-            if (e != hipSuccess)
-                return hip_status(e, "BC6 fold launch");
-        }
     } else {
     TrainDesc d{};
     d.mlp = mlp_desc(&p->mlp);

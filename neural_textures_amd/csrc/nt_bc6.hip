@@ -235,15 +235,15 @@ hipError_t launch_bc6_init(const Bc6InitDesc &d, hipStream_t s)
 
 // ---- the BC6 block phase on the fused train kernel ------------------------------------
 
-// The grid of a launch-wide block number (grids take consecutive ranges of blocks).
-__device__ __forceinline__ int bc6_phase_grid(const Bc6PhaseDesc &d, int64_t b)
+// The level of a launch-wide block number (levels take consecutive ranges of blocks).
+__device__ __forceinline__ int bc6_phase_level(const Bc6PhaseDesc &d, int64_t b)
 {
-    int gi = 0;
+    int li = 0;
 #pragma unroll
-    for (int k = 1; k < NT_MAX_GRIDS; ++k)
-        if (k < d.G && b >= d.grid[k].first_block)
-            gi = k;
-    return gi;
+    for (int k = 1; k < 2 * NT_MAX_GRIDS; ++k)
+        if (k < d.nlevels && b >= d.level[k].first_block)
+            li = k;
+    return li;
 }
 
 __device__ __forceinline__ int wrap_mod(int v, int n)
@@ -294,15 +294,17 @@ __global__ __launch_bounds__(256) void bc6_expand_kernel(Bc6PhaseDesc d)
     const int64_t b = t >> 4;
     if (b >= d.total_blocks)
         return;
-    const Bc6PhaseGrid &g = d.grid[bc6_phase_grid(d, b)];
-    // A grid's rectangle holds fewer than 2^31 blocks (its blocks fit 32-bit offsets).
+    const Bc6PhaseLevel &g = d.level[bc6_phase_level(d, b)];
+    // A level's rectangle holds fewer than 2^31 blocks (its texels fit 32-bit offsets).
     const int lb = (int)(b - g.first_block);
     const int ry = lb / g.nbx;
     const int bx = wrap_mod(g.bx0 + (lb - ry * g.nbx), g.nbu);
     const int by = wrap_mod(g.by0 + ry, g.nbv);
     const int pix = (int)(t & 15);
-    const Bc6Pixel<C> q = bc6_pixel<C>(g.params + ((int64_t)by * g.nbu + bx) * (4 * C + 18), pix);
     const int x = 4 * bx + (pix & 3), y = 4 * by + (pix >> 2);
+    if (x >= g.w || y >= g.h)
+        return; // a level narrower than a block (w or h < 4)
+    const Bc6Pixel<C> q = bc6_pixel<C>(g.params + ((int64_t)by * g.nbu + bx) * (4 * C + 18), pix);
     const int64_t o = ((int64_t)y * g.w + x) * C;
 #pragma unroll
     for (int ch = 0; ch < C; ++ch) {
@@ -355,20 +357,22 @@ __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
     const int64_t b = t >> 4;
     if (b >= d.total_blocks)
         return;
-    const Bc6PhaseGrid &g = d.grid[bc6_phase_grid(d, b)];
-    // A grid's rectangle holds fewer than 2^31 blocks (its blocks fit 32-bit offsets).
+    const Bc6PhaseLevel &g = d.level[bc6_phase_level(d, b)];
+    // A level's rectangle holds fewer than 2^31 blocks (its texels fit 32-bit offsets).
     const int lb = (int)(b - g.first_block);
     const int ry = lb / g.nbx;
     const int bx = wrap_mod(g.bx0 + (lb - ry * g.nbx), g.nbu);
     const int by = wrap_mod(g.by0 + ry, g.nbv);
     const int pix = (int)(t & 15);
     const int64_t blk = (int64_t)by * g.nbu + bx;
-    const int64_t o = ((int64_t)(4 * by + (pix >> 2)) * g.w + 4 * bx + (pix & 3)) * C;
+    const int x = 4 * bx + (pix & 3), y = 4 * by + (pix >> 2);
+    const bool inside = x < g.w && y < g.h; // a level narrower than a block (w or h < 4)
+    const int64_t o = ((int64_t)y * g.w + x) * C;
     float G[C];
     bool touched = false;
 #pragma unroll
     for (int ch = 0; ch < C; ++ch) {
-        G[ch] = g.tgrads[o + ch];
+        G[ch] = inside ? g.tgrads[o + ch] : 0.f;
         touched |= G[ch] != 0.f;
     }
     // Lanes of the block with a non-zero gradient (the block's 16-bit slice of the wave's).
@@ -413,26 +417,38 @@ __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
     }
 }
 
-hipError_t launch_bc6_expand(const Bc6PhaseDesc &d, hipStream_t s)
+template <template <int> class K>
+static hipError_t launch_phase(const Bc6PhaseDesc &d, hipStream_t s)
 {
     if (d.total_blocks <= 0)
         return hipSuccess;
-    if (d.C != 3)
+    const dim3 grid((unsigned)((d.total_blocks * 16 + 255) / 256));
+    switch (d.C) {
+    case 3:
+        hipLaunchKernelGGL(K<3>::kernel, grid, dim3(256), 0, s, d);
+        break;
+    case 8:
+        hipLaunchKernelGGL(K<8>::kernel, grid, dim3(256), 0, s, d);
+        break;
+    case 16:
+        hipLaunchKernelGGL(K<16>::kernel, grid, dim3(256), 0, s, d);
+        break;
+    default:
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(bc6_expand_kernel<3>, dim3((unsigned)((d.total_blocks * 16 + 255) / 256)), dim3(256), 0, s,
-                       d);
+    }
     return hipGetLastError();
 }
+template <int C>
+struct ExpandK {
+    static constexpr auto kernel = bc6_expand_kernel<C>;
+};
+template <int C>
+struct FoldK {
+    static constexpr auto kernel = bc6_fold_kernel<C>;
+};
 
-hipError_t launch_bc6_fold(const Bc6PhaseDesc &d, hipStream_t s)
-{
-    if (d.total_blocks <= 0)
-        return hipSuccess;
-    if (d.C != 3)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(bc6_fold_kernel<3>, dim3((unsigned)((d.total_blocks * 16 + 255) / 256)), dim3(256), 0, s,
-                       d);
-    return hipGetLastError();
-}
+hipError_t launch_bc6_expand(const Bc6PhaseDesc &d, hipStream_t s) { return launch_phase<ExpandK>(d, s); }
+
+hipError_t launch_bc6_fold(const Bc6PhaseDesc &d, hipStream_t s) { return launch_phase<FoldK>(d, s); }
 
 } // namespace ntk

@@ -228,28 +228,29 @@ struct Bc6InitDesc {
     int64_t start[kMaxExpandLevels + 1];
 };
 
-// BC6 block phase on the fused train kernel (NT_BLOCK_FEATURES, NT_FINALIZE with the
-// reference network's four 3-channel grids, region sampling). Per grid, the block records
-// of mip 0 under a rectangle of blocks that holds every footprint of the step are expanded
-// to fp32 texels in the workspace ([y * w + x][C], the unconstrained layout; their
-// gradients cleared); the fused unconstrained kernel trains on those texels; the fold then
-// turns each block's texel gradients into its record's endpoint and pixel-index gradients
-// (train.cu:373-458), which are linear in the texel gradient.
-struct Bc6PhaseGrid {
-    const float *params; // mip-0 block records, 4C + 18 floats each
-    float *grads;        // mip-0 block-gradient records, 4C + 16 floats each
+// BC6 block phase (NT_BLOCK_FEATURES, NT_FINALIZE): per (grid, mip) level a step samples,
+// the block records under a rectangle of blocks that holds every footprint of the step are
+// expanded to fp32 texels in the workspace ([y * w + x][C], the unconstrained layout; their
+// gradients cleared); an unconstrained train step (the fused kernel or the general one)
+// trains on those texels; the fold then turns each block's texel gradients into its
+// record's endpoint and pixel-index gradients (train.cu:373-458), which are linear in the
+// texel gradient.
+struct Bc6PhaseLevel {
+    const float *params; // the level's block records, 4C + 18 floats each
+    float *grads;        // its block-gradient records, 4C + 16 floats each
     float *values;       // expanded texels (workspace), w * h * C floats
     float *tgrads;       // their gradients (workspace)
     int w, h, nbu, nbv;  // texels; blocks per row and column
-    int bx0, by0, nbx, nby; // block rectangle: origin (may lie outside the grid: wraps), size
-    int64_t first_block;    // first block of this grid in the launch's numbering
+    int bx0, by0, nbx, nby; // block rectangle: origin (may lie outside the level: wraps), size
+    int64_t first_block;    // first block of this level in the launch's numbering
 };
 struct Bc6PhaseDesc {
-    Bc6PhaseGrid grid[NT_MAX_GRIDS];
-    int G, C;
+    Bc6PhaseLevel level[2 * NT_MAX_GRIDS];
+    int nlevels, C;
     int64_t total_blocks;
-    // NT_LATENT_TOUCHED: the update log, in which the fold records each grid's block
-    // rectangle {bx0, bx1, by0, by1} (inclusive, before wrapping); NULL: none.
+    // NT_LATENT_TOUCHED with one level per grid (mip 0): the update log, in which the fold
+    // records each grid's block rectangle {bx0, bx1, by0, by1} (inclusive, before wrapping);
+    // NULL: none.
     struct UpdateLog *log;
     int32_t rect[NT_MAX_GRIDS][4];
 };

@@ -11,12 +11,13 @@
 // accumulators stay in registers across chunks. Bias gradients are row sums of the same
 // LDS tiles. Latent gradients of unconstrained latents are reduced per chunk on MFMA
 // (cell weights x input gradients over the chunk's samples) into an LDS footprint box that
-// covers every texel the block can touch, then flushed once with global float atomics;
-// BC6 block latents take per-sample global atomics. The MLP gradient of the workgroup goes
-// to a per-workgroup partial that a deterministic two-stage reduction adds to the network
-// gradients (no weight-gradient atomics). This kernel serves what nt_train16.hip does not:
-// BC6 block latents, the finalize pass, samples at a mip coordinate above 0, textures of
-// other sizes or pitches, the reference network's random texels.
+// covers every texel the block can touch, then flushed once with global float atomics.
+// The MLP gradient of the workgroup goes to a per-workgroup partial that a deterministic
+// two-stage reduction adds to the network gradients (no weight-gradient atomics). This
+// kernel serves what nt_train16.hip does not: samples at a mip coordinate above 0, textures
+// of other sizes or pitches, the reference network's random texels, config 1's 8-channel
+// network; BC6 block latents reach it through the BC6 phase (nt_bc6.hip) as unconstrained
+// steps on expanded texels.
 #include "nt_train_parts.hpp"
 
 #include <mutex>
@@ -219,61 +220,6 @@ __device__ __forceinline__ void gather_box16(const TrainDesc &d, const SampleFoo
             }
         }
         x[q] = acc;
-    }
-}
-
-// BC6 block record of texel (x, y) at mip 0 (train.cu:204-212, 240-261).
-struct Bc6Texel {
-    int64_t block;
-    int pix, part, bits;
-};
-__device__ __forceinline__ Bc6Texel bc6_locate(const GridDesc &gr, int C, int x, int y)
-{
-    Bc6Texel t;
-    const int nbu = (gr.w >> 2) > 0 ? (gr.w >> 2) : 1;
-    t.block = gr.block_off[0] + (int64_t)(y >> 2) * nbu + (x >> 2);
-    t.pix = ((y & 3) << 2) + (x & 3);
-    const float *rec = gr.block_params + t.block * (4 * C + 18);
-    const int partition = __float_as_int(rec[4 * C + 16]);
-    const int mode = __float_as_int(rec[4 * C + 17]);
-    t.part = (bc6_partition_mask(partition) >> t.pix) & 1;
-    t.bits = bc6_mode_bits(mode);
-    return t;
-}
-
-// BC6 latent gather (train.cu:341-369): `half += float` resolves to the fp16 operator+=, so
-// each corner's fp32 product is rounded to fp16 first and then added in fp16 (two
-// roundings, as the unconstrained path, train.cu:306-310).
-template <int C, int KQ>
-__device__ __forceinline__ void gather_bc6(const TrainDesc &d, const SampleFootprints &f, int g,
-                                           h8 (&x)[KQ])
-{
-#pragma unroll
-    for (int q = 0; q < KQ; ++q) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int feat = 16 * q + 8 * g + e;
-            _Float16 a = (_Float16)0.f;
-            if (feat < d.G * C) {
-                const int gi = feat / C, ch = feat % C;
-                int x0, y0;
-                float w[4];
-                pick_footprint(f, gi, x0, y0, w);
-                const GridDesc &gr = grid_ref(d, gi);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int tx = wrap_coord(x0 + (c & 1), gr.w);
-                    const int ty = wrap_coord(y0 + (c >> 1), gr.h);
-                    const Bc6Texel t = bc6_locate(gr, C, tx, ty);
-                    const float *rec = gr.block_params + t.block * (4 * C + 18);
-                    const float v = bc6_decompress(rec[2 * t.part * C + ch],
-                                                   rec[(2 * t.part + 1) * C + ch], t.bits,
-                                                   rec[4 * C + t.pix]);
-                    a = a + (_Float16)rn32(w[c] * v);
-                }
-            }
-            x[q][e] = a;
-        }
     }
 }
 
@@ -624,86 +570,6 @@ __device__ __forceinline__ void scatter_rows16(const TrainDesc &d, const SampleF
     }
 }
 
-// BC6 backward of one sample (train.cu:373-458) to global atomics, the lane's terms summed
-// before they are added: each of the four corners' pixel-weight gradient over the lane's
-// channels of one grid (its features run in grid order), and a channel's endpoint gradients
-// over consecutive corners of one block and partition (the same two addresses). The
-// reference adds every term on its own (three adds per corner and channel); the sums differ
-// only in the order of fp32 additions, which its atomics leave open too.
-template <int C, int KQ>
-__device__ __forceinline__ void scatter_bc6(const TrainDesc &d, const SampleFootprints &f,
-                                            const h8 (&dx)[KQ], int g)
-{
-    int cur = -1;
-    Bc6Texel t[4];
-    const float *rec[4];
-    float *grec[4];
-    float w[4], wacc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        t[c] = Bc6Texel{0, 0, 0, 0};
-        rec[c] = nullptr;
-        grec[c] = nullptr;
-        w[c] = wacc[c] = 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < KQ; ++q)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int feat = chained_feature(q, g, e);
-            if (feat >= d.G * C)
-                continue;
-            const float grad = (float)dx[q][e];
-            const int gi = feat / C, ch = feat % C;
-            if (gi != cur) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (cur >= 0 && wacc[c] != 0.f)
-                        global_add(grec[c] + 4 * C + t[c].pix, wacc[c]);
-                cur = gi;
-                int x0, y0;
-                pick_footprint(f, gi, x0, y0, w);
-                const GridDesc &gr = grid_ref(d, gi);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int tx = wrap_coord(x0 + (c & 1), gr.w);
-                    const int ty = wrap_coord(y0 + (c >> 1), gr.h);
-                    t[c] = bc6_locate(gr, C, tx, ty);
-                    rec[c] = gr.block_params + t[c].block * (4 * C + 18);
-                    grec[c] = gr.block_grads + t[c].block * (4 * C + 16);
-                    wacc[c] = 0.f;
-                }
-            }
-            float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int base = 2 * t[c].part;
-                const float xi = rec[c][4 * C + t[c].pix];
-                const float q0 = bc6_unquantize(rec[c][base * C + ch], t[c].bits);
-                const float q1 = bc6_unquantize(rec[c][(base + 1) * C + ch], t[c].bits);
-                const int hy = bc6_hy(bc6_y(q0, q1, xi));
-                const float dl_dy = ldexpf(w[c] * grad, hy - 24);
-                const float dy_dx = ldexpf(q1 - q0, 3);
-                const float alpha = ldexpf(xi, 3);
-                const float deibar = ldexpf(31.f / 64.f, 16 - t[c].bits);
-                wacc[c] += dl_dy * dy_dx;
-                a0 += ((1.f - alpha) * deibar) * dl_dy;
-                a1 += (alpha * deibar) * dl_dy;
-                const bool last = c == 3 || t[c + 1 < 4 ? c + 1 : 3].block != t[c].block ||
-                                  t[c + 1 < 4 ? c + 1 : 3].part != t[c].part;
-                if (last) {
-                    global_add(grec[c] + base * C + ch, a0);
-                    global_add(grec[c] + (base + 1) * C + ch, a1);
-                    a0 = a1 = 0.f;
-                }
-            }
-        }
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-        if (cur >= 0 && wacc[c] != 0.f)
-            global_add(grec[c] + 4 * C + t[c].pix, wacc[c]);
-}
-
 // Latent gradient scatter of one 128-sample chunk as an MFMA reduction over the samples
 // (train.cu:460-509 without atomics): per grid, the chunk's cell-box gradient is
 //   D[cell][ch] = sum_s W[cell][s] * dX0[s][ch]
@@ -847,7 +713,7 @@ __device__ __forceinline__ void scatter_reduce(const TrainDesc &d, const int (&c
     }
 }
 
-template <class S, int C, int TYPE>
+template <class S, int C>
 __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
 {
     using LY = TrainLayout<S>;
@@ -886,7 +752,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
         flo_x[gi] = gi < GM ? (int)floorf((float)(d.off_x + tx0) * (float)gr.w / (float)d.image_w - 0.5f) - 1 : 0;
         flo_y[gi] = gi < GM ? (int)floorf((float)(d.off_y + ty0) * (float)gr.h / (float)d.image_h - 0.5f) - 1 : 0;
     }
-    if constexpr (C == 16 && TYPE == NT_UNCONSTRAINED) {
+    if constexpr (C == 16) {
         if (d.vbox_floats > 0)
             load_value_box<GM>(d, (float4 *)vbox, flo_x, flo_y, tid);
     }
@@ -902,7 +768,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
     for (int l = 0; l < L; ++l)
         dbacc[l] = 0.f;
 
-    const bool mfma_scatter = TYPE == NT_UNCONSTRAINED && d.scatter_mfma;
+    const bool mfma_scatter = d.scatter_mfma;
     const int col = 32 * wave + c; // column of this lane's sample in the LDS transposes
     for (int chunk = 0; chunk < d.chunks_per_wg; ++chunk) {
         const int cx0 = d.off_x + tx0 + chunk * kChunkW, cy0 = d.off_y + ty0;
@@ -933,20 +799,12 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
             SampleFootprints fps;
             sample_footprints<GM>(d, u, v, fps);
             if (valid) {
-                if constexpr (TYPE == NT_UNCONSTRAINED && C == 16) {
-                    if (d.trilinear)
-                        gather_trilinear<C, KQ0>(d, u, v, g, x0);
-                    else if (d.vbox_floats > 0)
-                        gather_box16<KQ0>(d, fps, flo_x, flo_y, vbox, g, x0);
-                    else
-                        gather_unconstrained<C, KQ0>(d, fps, g, x0);
-                } else if constexpr (TYPE == NT_UNCONSTRAINED) {
-                    if (d.trilinear)
-                        gather_trilinear<C, KQ0>(d, u, v, g, x0);
-                    else
-                        gather_unconstrained<C, KQ0>(d, fps, g, x0);
-                } else
-                    gather_bc6<C, KQ0>(d, fps, g, x0);
+                if (d.trilinear)
+                    gather_trilinear<C, KQ0>(d, u, v, g, x0);
+                else if (C == 16 && d.vbox_floats > 0)
+                    gather_box16<KQ0>(d, fps, flo_x, flo_y, vbox, g, x0);
+                else
+                    gather_unconstrained<C, KQ0>(d, fps, g, x0);
             } else {
 #pragma unroll
                 for (int q = 0; q < KQ0; ++q)
@@ -1009,7 +867,7 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
         store_transposed<HQ, true>(dyt, dyh, col, g);
         store_transposed<KQ0, false>(xt, x0, col, g);
         h8 dx0[KQ0];
-        if constexpr (TYPE != NT_FINALIZE) {
+        {
             constexpr int MA = S::t32(S::K0);
             f16v acc[MA];
             layer_backward_dx<HQ, MA>(frags + S::bwd_off(0) * kWave, dyh, acc, lane);
@@ -1023,21 +881,17 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
         SampleFootprints fps;
         sample_footprints<GM>(d, rn32(u), rn32(v), fps);
         int cbx[NT_MAX_GRIDS], cby[NT_MAX_GRIDS];
-        if constexpr (TYPE == NT_UNCONSTRAINED) {
-            chunk_box<GM>(d, cx0, cy0, cbx, cby);
-            if (mfma_scatter && d.scatter_split)
-                scatter_write<S, C, GM>(d, fps, dx0, valid, cbx, cby, flo_x, flo_y, fp, sct, col, g);
-        }
+        chunk_box<GM>(d, cx0, cy0, cbx, cby);
+        if (mfma_scatter && d.scatter_split)
+            scatter_write<S, C, GM>(d, fps, dx0, valid, cbx, cby, flo_x, flo_y, fp, sct, col, g);
         __syncthreads();
         dw_phase<S, 0>(xt, dyt, dwacc, dbacc[0], wave, lane, tid);
-        if constexpr (TYPE == NT_UNCONSTRAINED) {
-            if (mfma_scatter && d.scatter_split)
-                scatter_reduce<S, C, GM>(d, cbx, cby, flo_x, flo_y, fp, sct, S::dw_total(), wave, lane);
-        }
+        if (mfma_scatter && d.scatter_split)
+            scatter_reduce<S, C, GM>(d, cbx, cby, flo_x, flo_y, fp, sct, S::dw_total(), wave, lane);
         __syncthreads();
 
         // ---- latent gradient scatter when it cannot share the layer-0 phase
-        if constexpr (TYPE == NT_UNCONSTRAINED) {
+        {
             if (d.trilinear) {
                 if (valid)
                     scatter_trilinear<C, KQ0>(d, rn32(u), rn32(v), dx0, g);
@@ -1062,15 +916,12 @@ __global__ __launch_bounds__(kTrainThreads) void train_kernel(TrainDesc d)
             } else if (valid) {
                 scatter_unconstrained<C, KQ0>(d, fps, flo_x, flo_y, fp, dx0, g);
             }
-        } else if constexpr (TYPE == NT_BLOCK_FEATURES) {
-            if (valid)
-                scatter_bc6<C, KQ0>(d, fps, dx0, g);
         }
     }
 
     __syncthreads();
     // ---- flush the latent footprint box
-    if constexpr (TYPE == NT_UNCONSTRAINED) {
+    {
         // Grid by grid (uniform descriptors), each grid's box spread over the threads.
 #pragma unroll
         for (int gi = 0; gi < GM; ++gi) {
@@ -1203,10 +1054,12 @@ hipError_t launch_reduce(const ReduceDesc &d, hipStream_t s)
     return hipGetLastError();
 }
 
-template <class S, int C, int TYPE>
+// The general kernel trains unconstrained latents; block records train through the BC6
+// phase (expanded texels, then the fold), which calls it as an unconstrained step.
+template <class S, int C>
 static hipError_t launch_one(const TrainDesc &d, int num_wg, size_t lds, hipStream_t s)
 {
-    auto k = train_kernel<S, C, TYPE>;
+    auto k = train_kernel<S, C>;
     // Raise the kernel's dynamic LDS limit to the whole 160 KB once (thread-safe).
     static std::once_flag once;
     static hipError_t configured = hipSuccess;
@@ -1219,19 +1072,6 @@ static hipError_t launch_one(const TrainDesc &d, int num_wg, size_t lds, hipStre
     return hipGetLastError();
 }
 
-template <class S, int C>
-static hipError_t launch_typed(int type, const TrainDesc &d, int num_wg, size_t lds, hipStream_t s)
-{
-    switch (type) {
-    case NT_UNCONSTRAINED:
-        return launch_one<S, C, NT_UNCONSTRAINED>(d, num_wg, lds, s);
-    case NT_BLOCK_FEATURES:
-        return launch_one<S, C, NT_BLOCK_FEATURES>(d, num_wg, lds, s);
-    default:
-        return launch_one<S, C, NT_FINALIZE>(d, num_wg, lds, s);
-    }
-}
-
 using ShapeRef = Shape<16, 32, 2>;
 using ShapeC1 = Shape<16, 64, 2>; // BASELINE config 1's network: one grid of 8 channels, 8 -> 64 -> 64 -> 3
 using ShapeC2 = Shape<32, 64, 2>;
@@ -1239,15 +1079,17 @@ using ShapeC4 = Shape<64, 64, 3>;
 
 hipError_t launch_train(int shape, int type, const TrainDesc &d, int num_wg, size_t lds, hipStream_t s)
 {
+    if (type != NT_UNCONSTRAINED)
+        return hipErrorInvalidValue;
     switch (shape) {
     case kShapeRef:
-        return launch_typed<ShapeRef, 3>(type, d, num_wg, lds, s);
+        return launch_one<ShapeRef, 3>(d, num_wg, lds, s);
     case kShapeC1:
-        return launch_typed<ShapeC1, 8>(type, d, num_wg, lds, s);
+        return launch_one<ShapeC1, 8>(d, num_wg, lds, s);
     case kShapeC2:
-        return launch_typed<ShapeC2, 16>(type, d, num_wg, lds, s);
+        return launch_one<ShapeC2, 16>(d, num_wg, lds, s);
     case kShapeC4:
-        return launch_typed<ShapeC4, 16>(type, d, num_wg, lds, s);
+        return launch_one<ShapeC4, 16>(d, num_wg, lds, s);
     default:
         return hipErrorInvalidValue;
     }

@@ -695,7 +695,37 @@ def test_train_step_at_mip_coordinate(lib, O, shape, z):
         assert np.all(got[g.grads == 0] == 0)
 
 
-SHAPES_TEX = {"ref": [3, 3, 1], "c2": [3, 3, 3], "c4": [4, 4, 4]}
+SHAPES_TEX = {"ref": [3, 3, 1], "c1": [3], "c2": [3, 3, 3], "c4": [4, 4, 4]}
+
+
+@pytest.mark.parametrize("shape", ["ref", "c1", "c2", "c4"])
+@pytest.mark.parametrize("z", [0.5, 1.0, 2.25, 9.0])
+def test_block_train_step_at_mip_coordinate(lib, O, shape, z):
+    """BC6 block records sampled at a mip coordinate z > 0: the reference's block sampler and
+    its backward blend mips floor(z) and floor(z) + 1 (train.cu:316-371, 373-458; z past the
+    last mip clamps to it, and mips narrower than a block hold one partial block). Both
+    levels are expanded, trained as unconstrained texels and folded back; MLP and block
+    gradients match the oracle's at the MLP bar."""
+    say(f"case: BC6 blocks {shape} at mip coordinate {z}")
+
+    def state():
+        x = make_state(shape, image=128, region=(64, 32), offset=(30, 61), seed=14, blocks=True)
+        rng = np.random.default_rng(15)
+        x.textures = [_texture_chain(128, n, rng, 5, 1.0 + 0.5 * k) for k, n in enumerate(SHAPES_TEX[shape])]
+        x.sample_mip = z
+        return x
+    st, alt = state(), state()
+    gs = gpu_workspace(lib, st.to_torch(), abi.NT_BLOCK_FEATURES)
+    oracle_step(O, st, abi.NT_BLOCK_FEATURES)
+    oracle_step(O, alt, abi.NT_BLOCK_FEATURES, accum_f32=True)
+    nt.check(lib.nt_train_step(C.byref(gs.params()), abi.NT_BLOCK_FEATURES, None))
+    sync()
+    check_train_grads(st, gs, alt, abi.NT_BLOCK_FEATURES)
+    for g in st.grids:  # some record beyond mip 0 is reached (z >= 1: none at mip 0)
+        rec = 4 * g.channels + 16
+        nb0 = (max(g.width >> 2, 1) * max(g.height >> 2, 1)) * rec
+        assert np.count_nonzero(g.block_grads[nb0:]) > 0
+        assert z < 1 or np.count_nonzero(g.block_grads[:nb0]) == 0
 
 
 # ---- one training-loop iteration in one call ---------------------------------------------------
