@@ -216,6 +216,47 @@ def test_dw_partials_rounded_to_fp16_per_warp():
         assert np.count_nonzero(st.net.bias_grads[0]) > 0
 
 
+def _forward_f32_sequential(net, x16):
+    """The forward of a batch [n, in] with each output's sum accumulated in float32 in input
+    order from the bias (fp16 products are exact in float32), ReLU on hidden layers, fp16
+    rounding per layer."""
+    cur = x16.astype(np.float32)
+    L = len(net.sizes) - 1
+    for l in range(L):
+        pin, pout = abi.pad16(net.sizes[l]), abi.pad16(net.sizes[l + 1])
+        W = net.weights[l].view(np.float16).astype(np.float32).reshape(pout, pin)
+        b = np.zeros(pout, np.float32)
+        b[:net.sizes[l + 1]] = net.biases[l].view(np.float16).astype(np.float32)
+        x = np.zeros((cur.shape[0], pin), np.float32)
+        x[:, :min(cur.shape[1], pin)] = cur[:, :pin]
+        a = np.broadcast_to(b, (cur.shape[0], pout)).astype(np.float32)
+        for k in range(pin):  # sequential in k, each step rounded to float32
+            a = (a + x[:, k:k + 1] * W[None, :, k]).astype(np.float32)
+        if l < L - 1:
+            a = np.where(a > 0, a, np.float32(0))
+        cur = a.astype(np.float16).astype(np.float32)
+    return cur
+
+
+def test_mlp_accum_f32_switch_is_float32_in_index_order():
+    """ntref_set_mlp_accum_f32(1): the forward sums accumulate in float32 in index order
+    (bit-exact against a numpy float32 restatement); off, the forward is the float64 one
+    (float64 GEMM, rounded once); on this batch the two orders differ on some outputs."""
+    rng = np.random.default_rng(21)
+    net = P.make_network([64, 64, 64, 64, 16], rng=rng, init="xavier")
+    count = 4096
+    x = rng.uniform(-1, 1, size=(count, 64)).astype(np.float16)
+    O.ntref_set_mlp_accum_f32(1)
+    try:
+        got = oracle_mlp_forward(net, x.view(np.uint16).copy(), count)
+    finally:
+        O.ntref_set_mlp_accum_f32(0)
+    assert np.array_equal(got, _forward_f32_sequential(net, x)[:, :16])
+    off = oracle_mlp_forward(net, x.view(np.uint16).copy(), count)
+    assert np.array_equal(off, _forward64(net, x).astype(np.float32)[:, :16])
+    assert not np.array_equal(off, got)
+
+
 # ---- lazy Adam (train.cu:521-816) -----------------------------------------------------
 
 def _adam_state(step, grads_w0):
