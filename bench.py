@@ -53,7 +53,7 @@ TRAIN_HBM_BYTES_PER_LAUNCH = {0: (7096.5 * 2.0 + 4181.4) * 1024,
 RANDOM_BYTES_PER_SAMPLE = {2: 2 * 4 * 64 * 3 + 16 * 9 * 4,    # 2,112
                            4: 4 * 4 * 64 * 3 + 16 * 12 * 4}   # 3,840
 TRAIN_HBM_BYTES_RANDOM = {2: (353554.2 * 2.0 + 138384.0) * 1024}  # same counters, config 2 random texels
-WORKLOADS = ("c4", "c2", "c2r", "c5", "c3", "c1", "cref", "cref2k", "crefbc6")
+WORKLOADS = ("c4", "c2", "c2r", "c4r", "c5", "c3", "c1", "cref", "cref2k", "crefbc6")
 
 
 def log(msg):
@@ -650,6 +650,11 @@ def main():
             e["workload"] = ("config 2 with NT_SAMPLES_RANDOM (BASELINE's 'random texels'): 262,144 "
                              "samples at uniformly random texels of the whole 2048^2 image")
             del st
+        elif w == "c4r":
+            st, e = train_entry(lib, nt, ev, 4, 10, 3, sample_mode=1)
+            e["workload"] = ("config 4 with NT_SAMPLES_RANDOM (BASELINE's 'random texels'): 1,048,576 "
+                             "samples at uniformly random texels of the whole 4096^2 image")
+            del st
         elif w == "c5":
             e = bench_decode(lib, nt, ev)
         elif w == "c3":
@@ -661,6 +666,7 @@ def main():
 
     head = entries[only[0]]
     names = {"c4": "train_config4", "c2": "train_config2", "c2r": "train_config2_random_texels",
+             "c4r": "train_config4_random_texels",
              "c5": "decode", "c3": "codec", "c1": "forward_config1", "cref": "train_reference_network",
              "cref2k": "train_reference_network_bcf2k", "crefbc6": "train_reference_network_bc6_blocks"}
     ms_head = head.get("ms_per_step", head.get("ms", head.get("encode_ms")))
@@ -680,7 +686,7 @@ def main():
         "config": {"workload": head.get("workload"), "batch": head.get("batch"),
                    "step": "nt_train_iteration (nt_train_step + nt_optimize_network + nt_optimize_latents, "
                            "the reduction and both optimizers in one launch)"
-                   if only[0] in ("c4", "c2", "c2r") else None},
+                   if only[0] in ("c4", "c2", "c2r", "c4r") else None},
         "roofline": head.get("roofline"),
     }
     if "ms_per_step_separate_calls" in head:

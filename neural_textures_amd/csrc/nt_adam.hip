@@ -461,6 +461,8 @@ hipError_t launch_optimize_step(const OptimizeStepDesc &d0, hipStream_t s)
     const int64_t n = d.lat.start[d.lat.nseg];
     // Block records: 256 records per workgroup pass (block_adam_body); texels: kAdamSpan.
     int64_t lat = d.lat.rec > 0 ? (n + 255) / 256 : (n + kAdamSpan - 1) / kAdamSpan;
+    if (d.lat_wg > 0 && d.lat_wg < lat)
+        lat = d.lat_wg;
     if (lat > 8192)
         lat = 8192;
     hipLaunchKernelGGL(optimize_step_kernel, dim3((unsigned)(d.nred + lat)), dim3(kOptCols * kOptGroups), 0, s, d);

@@ -1414,6 +1414,24 @@ int nt_train_iteration(const nt_params *p, nt_kernel_type type, void *stream)
         o.net.bm1[l] = net.bm1[l];
         o.net.bm2[l] = net.bm2[l];
     }
+    // The latent update's grid, sized for the rectangles this step logs (a logged step's
+    // work: 512 items per workgroup pass for texels, 256 record floats for block records).
+    if (p->latent_update == NT_LATENT_TOUCHED) {
+        int64_t items = 0;
+        if (plan.bc6 && type == NT_BLOCK_FEATURES && p->sample_mip == 0.f) {
+            for (int k = 0; k < plan.bc6d.nlevels; ++k)
+                items += (int64_t)plan.bc6d.level[k].nbx * plan.bc6d.level[k].nby * (4 * p->latents.channels + 16);
+            o.lat_wg = (int)std::min<int64_t>((items + 255) / 256, 8192);
+        } else if (!plan.bc6 && plan.use16 && type == NT_UNCONSTRAINED &&
+                   (p->latents.channels == 16 || p->latents.channels == 3)) {
+            for (int gi = 0; gi < p->latents.num_grids; ++gi) {
+                int r[4];
+                footprint_rect(p, p->latents.grids[gi].width, p->latents.grids[gi].height, r);
+                items += (int64_t)(r[1] - r[0] + 1) * (r[3] - r[2] + 1) * (p->latents.channels == 16 ? 4 : 1);
+            }
+            o.lat_wg = (int)std::min<int64_t>((items + 511) / 512, 8192);
+        }
+    }
     st = train_step_with(p, type, stream, plan, (uint8_t *)p->workspace, update_log(p), &o.red);
     if (st)
         return st;

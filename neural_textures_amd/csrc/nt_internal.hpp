@@ -422,6 +422,10 @@ struct OptimizeStepDesc {
     NetUpdateDesc net;
     LatentAdamDesc lat;
     int nred;
+    // Workgroups of the latent part: 0 sizes it for the dense scan; nt_train_iteration sizes
+    // it for the rectangles its own train step logs (the loops are grid-stride, so a dense
+    // fallback on that grid gives the same results).
+    int lat_wg;
 };
 hipError_t launch_optimize_step(const OptimizeStepDesc &d, hipStream_t s);
 // Logs a train step whose footprints are not recorded (the optimizer then updates every

@@ -99,7 +99,7 @@ def _touched(O, st):
     return masks
 
 
-def _check_grads(O, st, gs, alt):
+def _check_grads(O, st, gs, alt, latent_loose=1e-2, zero_floor=1e-3, outliers=1e-4):
     for l in range(st.net.num_layers):
         e = rel_err(to_np(gs.net.weight_grads[l]), st.net.weight_grads[l])
         say(f"  dW{l} rel err {e:.2e}")
@@ -111,7 +111,8 @@ def _check_grads(O, st, gs, alt):
         assert np.count_nonzero(g.grads) > 0
         e = rel_err(got, g.grads)
         say(f"  latent grad {gi} rel err {e:.2e}")
-        assert_close(got.reshape(-1, g.channels), g.grads, f"latent grad {gi} [texel, channel]", ga.grads)
+        assert_close(got.reshape(-1, g.channels), g.grads, f"latent grad {gi} [texel, channel]", ga.grads,
+                     loose=latent_loose, outliers=outliers)
         n0 = g.width * g.height * g.channels
         mip0_got = got[:n0].reshape(g.height, g.width, g.channels)
         # texels no footprint reaches stay exactly zero (as do mips > 0)
@@ -119,7 +120,7 @@ def _check_grads(O, st, gs, alt):
         # where the oracle's sum is exactly zero (fp16 loss gradients underflow at this N),
         # the GPU's is zero up to the same tolerance
         zero = g.grads == 0
-        assert np.all(np.abs(got[zero]) <= 1e-3 * np.abs(g.grads).max())
+        assert np.all(np.abs(got[zero]) <= zero_floor * np.abs(g.grads).max())
 
 
 @pytest.mark.parametrize("mode", [abi.NT_SAMPLES_REGION, abi.NT_SAMPLES_RANDOM], ids=["region", "random"])
@@ -197,6 +198,25 @@ def test_reference_network_bc6_phase_full_train_step(lib, O, ktype):
         # gradients that underflow at this N), the GPU's is zero up to the same tolerance
         zero = g.block_grads == 0
         assert np.all(np.abs(got[zero]) <= 1e-3 * np.abs(g.block_grads).max())
+
+
+def test_config4_random_texels_full_train_step(lib, O):
+    """Config 4 with NT_SAMPLES_RANDOM (BASELINE's 'random texels'): 1,048,576 samples at
+    uniformly random texels of the whole 4096^2 image, one full step against the oracle.
+
+    At this N the loss gradient fp16(2 w err / N) is about a third of the fp16 subnormal
+    quantum 2^-24 for err ~ 0.1, so most samples' dy are 0 or one quantum, and a one-ulp
+    difference in an MLP output moves a sample's dy by a whole quantum (100 %). With random
+    texels a grid-0 texel sums only ~4 corner contributions (about 62 in region mode), so such
+    a flip, which neither oracle makes at the same sample, shows in its element: the loose
+    per-element floor, and the bound on elements whose oracle sum is exactly zero (a sample
+    whose dy rounded to zero on one side and to a quantum on the other), are 5e-2 of
+    max|ref| here (measured worst: 2.4 %, 16 elements above 1e-2; norm-wise 9.3e-4), and
+    up to 10^-3 of the elements may leave the strict bound (grid 1, ~16 contributions per
+    texel: 1,099 of 5.6 M). A wrap column or tile seam (16 K elements) still fails."""
+    say("case: config 4 full step with random texels (1,048,576 samples over the whole 4096^2 image)")
+    st, gs, alt = _train_pair(lib, O, 4, abi.NT_SAMPLES_RANDOM)
+    _check_grads(O, st, gs, alt, latent_loose=5e-2, zero_floor=5e-2, outliers=1e-3)
 
 
 def test_config4_full_train_step(lib, O):
