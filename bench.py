@@ -52,7 +52,11 @@ TRAIN_HBM_BYTES_PER_LAUNCH = {0: (7096.5 * 2.0 + 4181.4) * 1024,
 # gradient read-modify-write (2 x that) + the targets' channels at 16 taps x 4 B.
 RANDOM_BYTES_PER_SAMPLE = {2: 2 * 4 * 64 * 3 + 16 * 9 * 4,    # 2,112
                            4: 4 * 4 * 64 * 3 + 16 * 12 * 4}   # 3,840
-TRAIN_HBM_BYTES_RANDOM = {2: (353554.2 * 2.0 + 138384.0) * 1024}  # same counters, config 2 random texels
+TRAIN_HBM_BYTES_RANDOM = {2: (353554.2 * 2.0 + 138384.0) * 1024,    # same counters, config 2 random texels
+                          4: (1733133.3 * 2.0 + 1039644.9) * 1024}  # and config 4 random texels
+# The BC6 block phase's train kernel (the reference network on texels expanded from its
+# BCf-2k block records), same counters.
+TRAIN_HBM_BYTES_BC6 = (9164.1 * 2.0 + 8478.2) * 1024
 WORKLOADS = ("c4", "c2", "c2r", "c4r", "c5", "c3", "c1", "cref", "cref2k", "crefbc6")
 
 
@@ -240,7 +244,7 @@ def train_entry(lib, nt, ev, cfg, steps, warmup, sample_mode=0, blocks=False):
     else:
         roof = {"kernel": kernel, "bound": "mfma", "achieved": achieved, "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s", "frac": achieved / PEAK_FP16_TFLOPS,
-                "traffic": None if blocks else TRAIN_HBM_BYTES_PER_LAUNCH.get(cfg),
+                "traffic": TRAIN_HBM_BYTES_BC6 if blocks else TRAIN_HBM_BYTES_PER_LAUNCH.get(cfg),
                 "flop_per_launch": flops}
     roof.update({"launch_ms_mean": kmean, "launch_ms_median": kmed})
     return st, {"value": n / (ms / 1e3), "unit": "texels/s", "ms_per_step": ms, "steps": steps, "batch": n,
