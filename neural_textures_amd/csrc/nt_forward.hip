@@ -522,9 +522,13 @@ __device__ __forceinline__ void sample_box16(const int4 *gtab, const int4 *tab, 
             const float2 wh = dims[gi * NT_MAX_MIPS + mips[mi]];
             const Footprint f = bilinear_footprint(u, v, wh.x, wh.y, mw[mi]);
             const int4 e = tab[gi * NT_MAX_MIPS + mips[mi]];
-            const int bw = e.y & 0xFFFF, bh = e.y >> 16;
-            // In the box by construction; the clamps only guard LDS addressing.
-            const int lx = min(max(f.x0 - e.z, 0), bw - 2), ly = min(max(f.y0 - e.w, 0), bh - 2);
+            const int bw = e.y & 0xFFFF;
+            // In the box by construction: the box origin is the footprint origin of the
+            // block's lowest position and its size covers the highest one's (box_origin,
+            // box_last, the same float operations), and the origin is monotone in the
+            // position (fma, a division by the image size, floor), so 0 <= lx <= bw - 2 and
+            // likewise for ly.
+            const int lx = f.x0 - e.z, ly = f.y0 - e.w;
             const uint4 *t = box + 2 * (e.x + ly * bw + lx);
             const int row = 2 * bw;
             fma_corner16(lo, hi, f.w[0], __builtin_bit_cast(h8, t[0]), __builtin_bit_cast(h8, t[1]));
@@ -607,24 +611,40 @@ __global__ __launch_bounds__(kFwdThreads, 3) void decode_box_kernel(DecodeBoxDes
             int s[2];
             bool valid[2];
             h8 x0[2][KQ0];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int t = t0 + k * kFwdWaves;
+            // Both lane groups sample pixel c of both tiles. Lane group g computes the
+            // position and mip of pixel c of tile g only (as forward_kernel<..., Decode16>,
+            // pixel index s); one v_permlane32_swap of the wave's halves per value then hands
+            // every lane both: the first result holds the lower half's values (tile 0) in
+            // every lane, the second the upper half's (tile 1).
+            float uvz[3][2];
+            {
+                const int t = t0 + g * kFwdWaves;
                 const int px = bx0 + 32 * (t % (kBoxBlockW / 32)) + c, py = by0 + t / (kBoxBlockW / 32);
-                valid[k] = px < d.image_w && py < d.image_h;
                 const int cx = min(px, d.image_w - 1), cy = min(py, d.image_h - 1);
-                s[k] = cy * d.image_w + cx;
-                // Position and mip as forward_kernel<..., Decode16> (pixel index s).
-                uint32_t st = mix_seed((uint32_t)s[k], d.seed);
+                uint32_t st = mix_seed((uint32_t)(cy * d.image_w + cx), d.seed);
                 const float jx = uniform01(st) - 0.5f;
                 const float jy = uniform01(st) - 0.5f;
                 const float zu = uniform01(st);
                 const float posx = clampf(fmaf(d.jitter, jx, (float)cx + 0.5f), 0.5f, (float)d.image_w - 0.5f);
                 const float posy = clampf(fmaf(d.jitter, jy, (float)cy + 0.5f), 0.5f, (float)d.image_h - 0.5f);
-                const float u = div_pow2(posx, (float)d.image_w, d.inv_w);
-                const float v = div_pow2(posy, (float)d.image_h, d.inv_h);
-                const float z = fmaf(d.mip_max - d.mip_min, zu, d.mip_min);
-                sample_box16<KQ0>(gtab, tab, dims, box, u, v, z, g, x0[k]);
+                const float mine[3] = {div_pow2(posx, (float)d.image_w, d.inv_w),
+                                       div_pow2(posy, (float)d.image_h, d.inv_h),
+                                       fmaf(d.mip_max - d.mip_min, zu, d.mip_min)};
+#pragma unroll
+                for (int i = 0; i < 3; ++i) {
+                    const uint32_t b = __float_as_uint(mine[i]);
+                    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+                    uvz[i][0] = __uint_as_float(r[0]);
+                    uvz[i][1] = __uint_as_float(r[1]);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int t = t0 + k * kFwdWaves;
+                const int px = bx0 + 32 * (t % (kBoxBlockW / 32)) + c, py = by0 + t / (kBoxBlockW / 32);
+                valid[k] = px < d.image_w && py < d.image_h;
+                s[k] = min(py, d.image_h - 1) * d.image_w + min(px, d.image_w - 1);
+                sample_box16<KQ0>(gtab, tab, dims, box, uvz[0][k], uvz[1][k], uvz[2][k], g, x0[k]);
             }
 
             f16v out[2][1];
