@@ -503,38 +503,47 @@ __device__ __forceinline__ int wrap_mod(int c, int size)
     return r < 0 ? r + size : r;
 }
 
+// Sampling record of (grid, mip), built per block: the LDS byte address of box texel
+// (0, 0) of the unwrapped grid (the box's first texel minus its origin, so that a
+// footprint origin (x0, y0) is at base + 32 x0 + y0 row), the box row in bytes, and the
+// mip's dimensions as floats (exact: they are below 2^24).
+struct BoxSample {
+    int base, row;
+    float w, h;
+};
+
+typedef __attribute__((address_space(3))) const uint4 lds_uint4;
+
 template <int G>
-__device__ __forceinline__ void sample_box16(const int4 *gtab, const int4 *tab, const float2 *dims,
-                                             const uint4 *box, float u, float v, float z, int g, h8 (&x)[G])
+__device__ __forceinline__ void sample_box16(const int *max_mip, const BoxSample *samp, float u, float v, float z,
+                                             int g, h8 (&x)[G])
 {
+    // Mip pair (train.cu:266-281, as mip_pair) with the grids' clamp bound precomputed.
+    const float fz = floorf(z);
+    const int base = (int)fz;
+    const float frac = z - fz;
 #pragma unroll
     for (int j = 0; j < G / 2; ++j) {
-        const int gi = 2 * j + g;
-        // Grid sizes from LDS (per tile) rather than kernel arguments kept live across the loop.
-        const int nmips = gtab[gi].z;
-        int mips[2];
-        float mw[2];
-        const int nm = mip_pair(nmips, z, mips, mw);
+        const int gi = 2 * j + g, top = max_mip[gi];
+        const int mips[2] = {min(max(base, 0), top), min(max(base + 1, 0), top)};
+        const float mw[2] = {1.f - frac, frac};
         h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
+        const int nm = frac > 0.f ? 2 : 1;
         for (int mi = 0; mi < nm; ++mi) {
-            // The mip's dimensions as floats from LDS (exact: they are below 2^24), not
-            // shifted and converted per pixel.
-            const float2 wh = dims[gi * NT_MAX_MIPS + mips[mi]];
-            const Footprint f = bilinear_footprint(u, v, wh.x, wh.y, mw[mi]);
-            const int4 e = tab[gi * NT_MAX_MIPS + mips[mi]];
-            const int bw = e.y & 0xFFFF;
+            const BoxSample q = samp[gi * NT_MAX_MIPS + mips[mi]];
+            const Footprint f = bilinear_footprint(u, v, q.w, q.h, mw[mi]);
             // In the box by construction: the box origin is the footprint origin of the
             // block's lowest position and its size covers the highest one's (box_origin,
             // box_last, the same float operations), and the origin is monotone in the
-            // position (fma, a division by the image size, floor), so 0 <= lx <= bw - 2 and
-            // likewise for ly.
-            const int lx = f.x0 - e.z, ly = f.y0 - e.w;
-            const uint4 *t = box + 2 * (e.x + ly * bw + lx);
-            const int row = 2 * bw;
+            // position (fma, a division by the image size, floor), so the footprint's
+            // 2 x 2 texels lie in the box (x0 and y0 are at least -1: 24-bit products).
+            const int a = q.base + 32 * f.x0 + __mul24(f.y0, q.row);
+            const lds_uint4 *t = (const lds_uint4 *)(size_t)(uint32_t)a;
+            const lds_uint4 *t2 = (const lds_uint4 *)(size_t)(uint32_t)(a + q.row);
             fma_corner16(lo, hi, f.w[0], __builtin_bit_cast(h8, t[0]), __builtin_bit_cast(h8, t[1]));
             fma_corner16(lo, hi, f.w[1], __builtin_bit_cast(h8, t[2]), __builtin_bit_cast(h8, t[3]));
-            fma_corner16(lo, hi, f.w[2], __builtin_bit_cast(h8, t[row]), __builtin_bit_cast(h8, t[row + 1]));
-            fma_corner16(lo, hi, f.w[3], __builtin_bit_cast(h8, t[row + 2]), __builtin_bit_cast(h8, t[row + 3]));
+            fma_corner16(lo, hi, f.w[2], __builtin_bit_cast(h8, t2[0]), __builtin_bit_cast(h8, t2[1]));
+            fma_corner16(lo, hi, f.w[3], __builtin_bit_cast(h8, t2[2]), __builtin_bit_cast(h8, t2[3]));
             // One mip level's reads at a time keeps the register peak down.
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -554,12 +563,14 @@ __global__ __launch_bounds__(kFwdThreads, 3) void decode_box_kernel(DecodeBoxDes
     float *bias = (float *)(smem + LY::bias_off);
     uint4 *box = (uint4 *)(smem + d.lds_box_off);
     __shared__ int4 tab[NT_MAX_GRIDS * NT_MAX_MIPS];
-    __shared__ float2 dims[NT_MAX_GRIDS * NT_MAX_MIPS];
-    __shared__ int4 gtab[NT_MAX_GRIDS];
+    __shared__ BoxSample samp[NT_MAX_GRIDS * NT_MAX_MIPS];
+    __shared__ int max_mip[NT_MAX_GRIDS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
+    // LDS byte address of the boxes.
+    const int box_addr = (int)(uint32_t)(size_t)(__attribute__((address_space(3))) unsigned char *)(smem + d.lds_box_off);
     stage_weights<S, true, true>(d.mlp, frags, bias, tid, kFwdThreads);
     if (tid < NT_MAX_GRIDS)
-        gtab[tid] = tid < d.G ? make_int4(d.grid[tid].w, d.grid[tid].h, d.grid[tid].num_mips, 0) : make_int4(1, 1, 1, 0);
+        max_mip[tid] = tid < d.G && d.grid[tid].num_mips > 0 ? d.grid[tid].num_mips - 1 : 0;
 
     const int nblocks = d.blocks_x * d.blocks_y;
     for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
@@ -578,8 +589,10 @@ __global__ __launch_bounds__(kFwdThreads, 3) void decode_box_kernel(DecodeBoxDes
                 }
             }
             tab[tid] = e;
-            dims[tid] = gi < d.G ? make_float2((float)mip_dim(d.grid[gi].w, m), (float)mip_dim(d.grid[gi].h, m))
-                                 : make_float2(1.f, 1.f);
+            const int bw = e.y & 0xFFFF;
+            samp[tid] = BoxSample{box_addr + 32 * (e.x - e.w * bw - e.z), 32 * bw,
+                                  gi < d.G ? (float)mip_dim(d.grid[gi].w, m) : 1.f,
+                                  gi < d.G ? (float)mip_dim(d.grid[gi].h, m) : 1.f};
         }
         __syncthreads();
         // Stage the boxes: texel k of box (gi, m) is global texel (origin + (k % bw, k / bw)),
@@ -644,7 +657,7 @@ __global__ __launch_bounds__(kFwdThreads, 3) void decode_box_kernel(DecodeBoxDes
                 const int px = bx0 + 32 * (t % (kBoxBlockW / 32)) + c, py = by0 + t / (kBoxBlockW / 32);
                 valid[k] = px < d.image_w && py < d.image_h;
                 s[k] = min(py, d.image_h - 1) * d.image_w + min(px, d.image_w - 1);
-                sample_box16<KQ0>(gtab, tab, dims, box, uvz[0][k], uvz[1][k], uvz[2][k], g, x0[k]);
+                sample_box16<KQ0>(max_mip, samp, uvz[0][k], uvz[1][k], uvz[2][k], g, x0[k]);
             }
 
             f16v out[2][1];
