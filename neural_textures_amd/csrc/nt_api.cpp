@@ -487,8 +487,17 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         d.group_bytes = (int)((d.tile_bytes + un + 15) & ~(size_t)15);
         return (size_t)d.group_off + (size_t)NG * d.group_bytes;
     };
+    // The kernel runs each wave's scatter-reduction tasks (16-cell tiles of the cell boxes)
+    // in one pass of two: at most eight (so at most 128 cells per box, and box coordinates
+    // below 256).
+    auto tasks = [&]() {
+        int n = 0;
+        for (int gi = 0; gi < G; ++gi)
+            n += (d.grid[gi].ncell + 15) / 16;
+        return n;
+    };
     size_t lds = layout();
-    while (!random && lds > kMaxLds) {
+    while (!random && (lds > kMaxLds || tasks() > 8)) {
         int big = -1;
         for (int gi = 0; gi < G; ++gi)
             if (d.grid[gi].ncell > 0 && (big < 0 || d.grid[gi].ncell > d.grid[big].ncell))

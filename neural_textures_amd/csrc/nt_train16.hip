@@ -846,6 +846,44 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     }
     float *sbox = (float *)(smem + d.box_lds_off); // per-sample scatter boxes (box_floats)
 
+    // The scatter reduction's tasks (one per grid and 16-cell tile of its chunk cell box,
+    // at most eight: the planner keeps no more) go to wave k % 4, so this wave runs tasks
+    // wave and wave + 4. Lane group grp of a task holds cells 16 t + 4 r + grp, r = 0..3;
+    // their offsets in the cell box are the same for every chunk. With registers to spare
+    // (one group) they are computed once: one byte each of cx and cy (the planner keeps at
+    // most 128 cells per grid, so both are below 255), two cells per register, 0xFFFF for a
+    // cell past the box; two groups (256 registers a wave) compute them per chunk.
+    int ntask = 0, task_g[2] = {0, 0}, task_t[2] = {0, 0};
+    uint32_t task_cell[2][2] = {{0u, 0u}, {0u, 0u}};
+    if constexpr (!RND && PF) {
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+            ntask += (d.grid[gi].ncell + 15) >> 4;
+        const int grp = lane >> 4;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            int k = wave + 4 * j, gsel = 0;
+#pragma unroll
+            for (int gi = 0; gi + 1 < G; ++gi) {
+                const int n = (d.grid[gi].ncell + 15) >> 4;
+                if (gsel == gi && k >= n) {
+                    k -= n;
+                    gsel = gi + 1;
+                }
+            }
+            task_g[j] = __builtin_amdgcn_readfirstlane(gsel);
+            task_t[j] = __builtin_amdgcn_readfirstlane(k);
+            const int cbw = sreg(d.grid[task_g[j]].cb_w), ncell = sreg(d.grid[task_g[j]].ncell);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int cell = 16 * task_t[j] + 4 * r + grp;
+                const int cy = cbw > 0 ? cell / cbw : 0;
+                const uint32_t e = cell < ncell ? (uint32_t)(cell - cy * cbw) | ((uint32_t)cy << 8) : 0xFFFFu;
+                task_cell[j][r >> 1] |= e << (16 * (r & 1));
+            }
+        }
+    }
+
     f16v dwacc[LY::slots];
 #pragma unroll
     for (int j = 0; j < LY::slots; ++j)
@@ -1178,30 +1216,37 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
             if (d.gather_grids > 0)
                 gather_records<NG>(d, sbox, d.off_x + tx0 + chunk * kChunkW, d.off_y + ty0, tx0, ty0, tid);
         }
-        // Part 2: one task per (grid, 16-cell tile); task k goes to wave k % 4. A wave takes
+        // Part 2: one task per (grid, 16-cell tile), this wave's two (above). A wave takes
         // its tasks two at a time with their LDS reads and MFMAs interleaved (the 4-grid
         // network has five tasks: one wave runs two, and their latencies overlap).
         {
-            int total = 0;
+            int total = ntask;
+            if constexpr (!PF) {
+                total = 0;
 #pragma unroll
-            for (int gi = 0; gi < G; ++gi)
-                total += (d.grid[gi].ncell + 15) >> 4;
+                for (int gi = 0; gi < G; ++gi)
+                    total += (d.grid[gi].ncell + 15) >> 4;
+            }
             const int i16 = lane & 15, grp = lane >> 4;
-            for (int k0 = wave; k0 < total; k0 += 8) {
-                int tg[2], tt[2];
+            // One pass with at most eight tasks (the planner's bound); two groups keep the
+            // general loop.
+            for (int k0 = wave; k0 < total; k0 += PF ? total : 8) {
+                int tg[2] = {task_g[0], task_g[1]}, tt[2] = {task_t[0], task_t[1]};
+                if constexpr (!PF) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    int k = k0 + 4 * j, gsel = 0;
+                    for (int j = 0; j < 2; ++j) {
+                        int k = k0 + 4 * j, gsel = 0;
 #pragma unroll
-                    for (int gi = 0; gi + 1 < G; ++gi) {
-                        const int n = (d.grid[gi].ncell + 15) >> 4;
-                        if (gsel == gi && k >= n) {
-                            k -= n;
-                            gsel = gi + 1;
+                        for (int gi = 0; gi + 1 < G; ++gi) {
+                            const int n = (d.grid[gi].ncell + 15) >> 4;
+                            if (gsel == gi && k >= n) {
+                                k -= n;
+                                gsel = gi + 1;
+                            }
                         }
+                        tg[j] = __builtin_amdgcn_readfirstlane(gsel);
+                        tt[j] = __builtin_amdgcn_readfirstlane(k);
                     }
-                    tg[j] = __builtin_amdgcn_readfirstlane(gsel);
-                    tt[j] = __builtin_amdgcn_readfirstlane(k);
                 }
                 const bool two = k0 + 4 < total;
                 f4v acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -1261,7 +1306,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                     // The task's grid fields once, every address before any atomic (no
                     // reloads of the fields inside the guarded stores).
                     const Grid16 &q = d.grid[tg[j]];
-                    const int w = sreg(q.w), h = sreg(q.h), cbw = sreg(q.cb_w), ncell = sreg(q.ncell);
+                    const int w = sreg(q.w), h = sreg(q.h), cbw = sreg(q.cb_w), cbh = sreg(q.cb_h);
+                    const int ncell = sreg(q.ncell);
                     const float icbw = sreg(q.inv_cb_w);
                     float *grads = sreg(q.grads);
                     const int bx = (int)floorf(fmaf((float)cx0, sreg(q.rx), -0.5f));
@@ -1270,14 +1316,32 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
                     bool ok[4];
                     // D column i16 is dX0 feature dx_col0(grid) + i16, channel cl of this grid.
                     const int cl = i16 - (C * tg[j] - dx_col0<C>(tg[j]));
+                    if constexpr (PF) {
+                        // The lane's cells from the launch's table; a cell box wholly inside
+                        // the grid (the chunk is not at a wrapping edge) needs no wrap.
+                        const bool inside = bx >= 0 && by >= 0 && bx + cbw <= w && by + cbh <= h;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int cell = 16 * tt[j] + 4 * r + grp; // D row 4grp + r holds column 16t + 4grp + r
-                        const int cy = (int)(((float)cell + 0.5f) * icbw);
-                        const int cxx = cell - cy * cbw;
-                        const int tx = wrap_near(bx + cxx, w), ty = wrap_near(by + cy, h);
-                        off[r] = (uint32_t)(ty * w + tx) * (uint32_t)C + (uint32_t)cl;
-                        ok[r] = cell < ncell && (C == 16 || (unsigned)cl < (unsigned)C) && acc[j][r] != 0.f;
+                        for (int r = 0; r < 4; ++r) {
+                            // D row 4grp + r: cell 16t + 4r + grp
+                            const uint32_t e = task_cell[j][r >> 1] >> (16 * (r & 1));
+                            int tx = bx + (int)(e & 0xFFu), ty = by + (int)((e >> 8) & 0xFFu);
+                            if (!inside) {
+                                tx = wrap_near(tx, w);
+                                ty = wrap_near(ty, h);
+                            }
+                            off[r] = __umul24((uint32_t)ty, (uint32_t)w) * (uint32_t)C + (uint32_t)(tx * C + cl);
+                            ok[r] = (e & 0xFFFFu) != 0xFFFFu && (C == 16 || (unsigned)cl < (unsigned)C) && acc[j][r] != 0.f;
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int cell = 16 * tt[j] + 4 * r + grp; // D row 4grp + r holds column 16t + 4grp + r
+                            const int cy = (int)(((float)cell + 0.5f) * icbw);
+                            const int cxx = cell - cy * cbw;
+                            const int tx = wrap_near(bx + cxx, w), ty = wrap_near(by + cy, h);
+                            off[r] = (uint32_t)(ty * w + tx) * (uint32_t)C + (uint32_t)cl;
+                            ok[r] = cell < ncell && (C == 16 || (unsigned)cl < (unsigned)C) && acc[j][r] != 0.f;
+                        }
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
