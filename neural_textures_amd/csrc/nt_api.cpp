@@ -419,7 +419,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     // Region: tiles of 64 x 8NG positions. Random texels: tiles of 512 consecutive samples
     // (of the position-sorted order).
     d.tiles_x = random ? 1 : (rw + 4 * kChunkW - 1) / (4 * kChunkW);
-    const int64_t tiles_y = random ? ((int64_t)p->num_samples + 4 * kChunk - 1) / (4 * kChunk)
+    const int64_t tiles_y = random ? ((int64_t)p->num_samples + 4 * kChunk * NG - 1) / (4 * kChunk * NG)
                                    : (rows + kChunkH * NG - 1) / (kChunkH * NG);
     if ((int64_t)d.tiles_x * tiles_y > (1 << 30))
         return;
@@ -557,8 +557,13 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         lds = (size_t)d.box_lds_off + ((size_t)d.box_floats + slot_floats) * 4;
     // The second group's region carries its dW accumulators to the first at the end.
     const size_t handoff = (size_t)train16_slots(plan->shape) * 17 * kTrainThreads * 4;
-    if (NG == 2 && (size_t)d.group_bytes < handoff)
-        return;
+    if (NG == 2 && (size_t)d.group_bytes < handoff) {
+        // Random texels keep no tile or cell box in the group regions: enlarge them.
+        if (!random)
+            return;
+        d.group_bytes = (int)((handoff + 15) & ~(size_t)15);
+        lds = (size_t)d.group_off + (size_t)NG * d.group_bytes;
+    }
     // The prologue stages the fp16 weight matrices in the group regions.
     if (lds > kMaxLds || train16_raw_bytes(plan->shape) > (size_t)NG * d.group_bytes)
         return;

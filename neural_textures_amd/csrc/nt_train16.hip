@@ -405,6 +405,52 @@ __device__ __forceinline__ void taps_targets(const Train16Desc &d, const LaneTap
     }
 }
 
+// Two groups (256 registers a wave): the same targets with each texture's 16 taps loaded
+// just before its fmas, so that only one texture's taps are live at a time.
+__device__ __forceinline__ void taps_targets_late(const Train16Desc &d, float u, float v, int g, float (&t)[8],
+                                                  float (&wt)[8])
+{
+    float wx[4], wy[4];
+    const int gx0 = cr_axis(u, d.image_w, wx), gy0 = cr_axis(v, d.image_h, wy);
+    int xo[4], yo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        xo[i] = wrap_near(gx0 + i, d.image_w);
+        yo[i] = wrap_near(gy0 + i, d.image_h) * d.image_w;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int ti = g + 2 * j;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (ti < d.ntex) {
+            const float4 *tex = (const float4 *)(g ? sreg(d.tex[2 * j + 1]) : sreg(d.tex[2 * j]));
+            float4 p[16];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    p[4 * jj + i] = load_global(tex + (uint32_t)(yo[jj] + xo[i]));
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float wxy = wx[i] * wy[jj];
+                    acc[0] = fmaf(p[4 * jj + i].x, wxy, acc[0]);
+                    acc[1] = fmaf(p[4 * jj + i].y, wxy, acc[1]);
+                    acc[2] = fmaf(p[4 * jj + i].z, wxy, acc[2]);
+                    acc[3] = fmaf(p[4 * jj + i].w, wxy, acc[3]);
+                }
+        }
+        const int nch = ti < d.ntex ? (g ? sreg(d.tex_nch[2 * j + 1]) : sreg(d.tex_nch[2 * j])) : 0;
+        const float lw = g ? sreg(d.tex_w[2 * j + 1]) : sreg(d.tex_w[2 * j]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            t[4 * j + r] = r < nch ? acc[r] : 0.f;
+            wt[4 * j + r] = r < nch ? lw : 1.f;
+        }
+    }
+}
+
 // Bilinear footprint at mip 0 of a w x h grid (train.cu:284-303, z = 0).
 __device__ __forceinline__ Footprint footprint16(int w, int h, float u, float v)
 {
@@ -759,7 +805,6 @@ __device__ __forceinline__ void gather_records(const Train16Desc &d, float *sbox
 template <class S, int C, int NG, bool RND>
 __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc d)
 {
-    static_assert(!RND || NG == 1, "random texels run one group per workgroup");
     static_assert(!RND || C == 16, "random texels are built for 16-channel grids");
     using LY = T16Layout<S, NG>;
     // Grids: one per 16 inputs with 16 channels; the 3-channel network has four.
@@ -926,8 +971,9 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         uint32_t sidx = (uint32_t)sy * (uint32_t)d.region_w + (uint32_t)sx;
         bool valid = sx < d.region_w && sidx < (uint32_t)d.num_samples;
         if constexpr (RND) {
-            // Sample 512 b + 128 chunk + 32 wave + c: tiles of consecutive samples.
-            sidx = (((uint32_t)b * 4u + (uint32_t)chunk) * 4u + (uint32_t)wave) * 32u + (uint32_t)c;
+            // Sample 512 (NG b + gr) + 128 chunk + 32 wave + c: tiles of consecutive samples.
+            sidx = (((((uint32_t)b * NG + (uint32_t)gr) * 4u + (uint32_t)chunk) * 4u + (uint32_t)wave) * 32u) +
+                   (uint32_t)c;
             valid = sidx < (uint32_t)d.num_samples;
         }
         uint32_t st = mix_seed(sidx, d.step);
@@ -940,8 +986,11 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         const float py = clampf((float)ty + 0.5f + jy, 0.5f, (float)d.image_h - 0.5f);
         const float u = div_pow2(px, (float)d.image_w, d.inv_w);
         const float v = div_pow2(py, (float)d.image_h, d.inv_h);
+        // One group (registers to spare) issues the taps here, so that their latency overlaps
+        // the gathers and the MLP; two groups issue them before use and hide the latency with
+        // the other group's wave.
         LaneTaps taps;
-        if constexpr (RND)
+        if constexpr (RND && PF)
             issue_taps(d, u, v, g, taps);
 
         h8 x0[KQ0];
@@ -980,8 +1029,10 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         h8 dyo[1];
         {
             float tgt[8], tw[8];
-            if constexpr (RND)
+            if constexpr (RND && PF)
                 taps_targets(d, taps, g, tgt, tw);
+            else if constexpr (RND)
+                taps_targets_late(d, u, v, g, tgt, tw);
             else
                 lane_targets16<PF>(d, tile, cx0, cy0, u, v, g, tgt, tw);
             float grd[8];
@@ -1494,7 +1545,7 @@ static hipError_t launch16(const Train16Desc &d, size_t lds, hipStream_t s)
 int train16_groups(int shape, bool random_texels)
 {
     if (random_texels)
-        return shape == kShapeC2 || shape == kShapeC4 ? 1 : 0;
+        return shape == kShapeC2 ? 2 : shape == kShapeC4 ? 1 : 0;
     return shape == kShapeRef || shape == kShapeC2 ? 2 : shape == kShapeC4 ? 1 : 0;
 }
 
@@ -1552,7 +1603,7 @@ hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream
     case kShapeRef:
         return d.random_texels ? hipErrorInvalidValue : launch16<ShapeRef, 3, 2, false>(d, lds, s);
     case kShapeC2:
-        return d.random_texels ? launch16<ShapeC2, 16, 1, true>(d, lds, s)
+        return d.random_texels ? launch16<ShapeC2, 16, 2, true>(d, lds, s)
                                : launch16<ShapeC2, 16, 2, false>(d, lds, s);
     case kShapeC4:
         return d.random_texels ? launch16<ShapeC4, 16, 1, true>(d, lds, s)
