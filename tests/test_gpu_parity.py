@@ -252,13 +252,15 @@ def test_train_step_scatter_out_of_box_paths(lib, O, shape):
 
 
 @pytest.mark.parametrize("shape,region,max_wg", [("ref", (64, 32), 0), ("c1", (64, 32), 0), ("c2", (64, 32), 0),
-                                                 ("c4", (64, 32), 0), ("c2", (50, 13), 2), ("c4", (100, 7), 1)],
-                         ids=["ref", "c1", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg"])
+                                                 ("c4", (64, 32), 0), ("c2", (50, 13), 2), ("c4", (100, 7), 1),
+                                                 ("c2", (100, 30), 2)],
+                         ids=["ref", "c1", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg", "c2-3tiles-2wg"])
 def test_train_step_random_texels(lib, O, shape, region, max_wg):
     """NT_SAMPLES_RANDOM: samples anywhere in the image (the 16-channel kernel with taps
     from global memory and per-sample corner atomics; the general kernel for the reference
     network); gradients match the oracle's at the MLP tolerance. Ragged regions leave
-    partial tiles; one or two workgroups walk every tile."""
+    partial tiles; one or two workgroups walk every tile (config 2 runs two groups of 512
+    samples per tile: 3,000 samples are three tiles, two of them on one workgroup)."""
     say(f"case: train {shape} random texels region {region} max workgroups {max_wg}")
     nt.check(lib.nt_set_test_hooks(max_wg, 0))
     try:
