@@ -553,7 +553,7 @@ __device__ __forceinline__ void sample_box16(const int *max_mip, const BoxSample
 }
 
 template <class S>
-__global__ __launch_bounds__(kFwdThreads, 3) void decode_box_kernel(DecodeBoxDesc d)
+__global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDesc d)
 {
     using LY = FwdLayout<S>;
     constexpr int L = S::L, NH = S::NH, KQ0 = S::K0 / 16, HQ = S::H / 16, HA = S::t32(S::H);
