@@ -377,6 +377,9 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             return;
     Train16Desc &d = plan->t16;
     d = Train16Desc{};
+    // The one-group (config 4) kernel: its single wave per SIMD runs both lane groups' taps
+    // in turn (two waves per SIMD cover the imbalance, measured: no gain for them).
+    d.split3 = !random && NG == 1 && p->num_textures == 3;
     int prefix = 0;
     bool mapped[NT_MAX_OUTPUTS] = {};
     int8_t row_out[NT_MAX_OUTPUTS];
@@ -393,7 +396,10 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
         d.four_channels |= nch == 4;
         d.tex_w[t] = x.loss_weight;
         for (int ch = 0; ch < nch; ++ch) {
-            row_out[4 * t + ch] = (int8_t)(prefix + ch);
+            // The third of three textures: channels 0, 1 on rows 8, 9 (lane group 0), 2, 3
+            // on rows 12, 13 (lane group 1).
+            const int row = d.split3 && t == 2 ? (ch < 2 ? 8 + ch : 12 + ch - 2) : 4 * t + ch;
+            row_out[row] = (int8_t)(prefix + ch);
             mapped[prefix + ch] = true;
         }
         prefix += nch;

@@ -126,6 +126,10 @@ struct Train16Desc {
     float tex_w[4];      // loss weight of texture t's rows
     int ntex;
     int four_channels;   // some texture has four channels
+    // Three textures, region positions, one group: lane group g takes texture g whole and
+    // channels 2g, 2g + 1 of texture 2 (output rows 8 + 4g + r), so that both groups read
+    // six channels' taps instead of one group eight and the other four.
+    int split3;
     int image_w, image_h, off_x, off_y, region_w, num_samples;
     uint32_t step;
     // 1/image_w, 1/image_h, 1/num_samples where that is a power of two (a product with the

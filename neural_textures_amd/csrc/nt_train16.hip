@@ -293,9 +293,44 @@ __device__ __forceinline__ void cr_taps(const float4 *base, const float (&wx)[4]
         }
 }
 
+// Two channels (an 8-byte half of each tap's float4, `half` 0 or 1) of one texture.
+template <bool PF>
+__device__ __forceinline__ void cr_taps2(const float4 *base, int half, const float (&wx)[4], const float (&wy)[4],
+                                         float (&acc)[4])
+{
+    const float2 *b2 = (const float2 *)base + half;
+    if constexpr (!PF) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 q = b2[2 * (jj * kT16TileStride + i)];
+                const float wxy = wx[i] * wy[jj];
+                acc[0] = fmaf(q.x, wxy, acc[0]);
+                acc[1] = fmaf(q.y, wxy, acc[1]);
+            }
+        return;
+    }
+    float2 p[4][4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            p[jj][i] = b2[2 * (jj * kT16TileStride + i)];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float wxy = wx[i] * wy[jj];
+            acc[0] = fmaf(p[jj][i].x, wxy, acc[0]);
+            acc[1] = fmaf(p[jj][i].y, wxy, acc[1]);
+        }
+}
+
 // Catmull-Rom targets and loss weights of the lane's eight output rows 8j + 4g + ch,
-// j = 0, 1: texture t = g + 2j, channel ch (train.cu:105-157; 16 taps, exact weights,
-// the fp32 fma order of the scalar restatement). Rows without a texture channel are the
+// j = 0, 1: texture t = g + 2j, channel ch; with three textures (split3) rows 8 + 4g + ch
+// are channels 2g + ch of texture 2 (train.cu:105-157; 16 taps, exact weights, the fp32
+// fma order of the scalar restatement). Rows without a texture channel are the
 // reference's unused outputs: target 0, weight 1.
 template <bool PF>
 __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float4 *tile, int cx0, int cy0,
@@ -307,9 +342,26 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
     const bool inside = x0 >= 0 && x0 + 3 < kT16TileW && y0 >= 0 && y0 + 3 < kT16TileH;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int ti = g + 2 * j;
+        const bool half = PF && j == 1 && d.split3; // channels 2g, 2g + 1 of texture 2 (one group)
+        const int ti = half ? 2 : g + 2 * j;
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        if (ti < d.ntex) {
+        if (half) {
+            if (inside) {
+                cr_taps2<PF>(tile + 2 * kT16TileSlots + y0 * kT16TileStride + x0, g, wx, wy, acc);
+            } else {
+                const float *tex = sreg(d.tex[2]);
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int y = wrap_coord(gy0 + jj, d.image_h);
+                    for (int i = 0; i < 4; ++i) {
+                        const int x = wrap_coord(gx0 + i, d.image_w);
+                        const float2 p = load_global((const float2 *)(tex + ((int64_t)y * d.image_w + x) * 4) + g);
+                        const float wxy = wx[i] * wy[jj];
+                        acc[0] = fmaf(p.x, wxy, acc[0]);
+                        acc[1] = fmaf(p.y, wxy, acc[1]);
+                    }
+                }
+            }
+        } else if (ti < d.ntex) {
             if (inside) {
                 const float4 *base = tile + ti * kT16TileSlots + y0 * kT16TileStride + x0;
                 if (d.four_channels)
@@ -332,8 +384,12 @@ __device__ __forceinline__ void lane_targets16(const Train16Desc &d, const float
                 }
             }
         }
-        const int nch = ti < d.ntex ? (g ? sreg(d.tex_nch[2 * j + 1]) : sreg(d.tex_nch[2 * j])) : 0;
-        const float lw = g ? sreg(d.tex_w[2 * j + 1]) : sreg(d.tex_w[2 * j]);
+        int nch = ti < d.ntex ? (g ? sreg(d.tex_nch[2 * j + 1]) : sreg(d.tex_nch[2 * j])) : 0;
+        float lw = g ? sreg(d.tex_w[2 * j + 1]) : sreg(d.tex_w[2 * j]);
+        if (half) {
+            nch = min(max(sreg(d.tex_nch[2]) - 2 * g, 0), 2);
+            lw = sreg(d.tex_w[2]);
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             t[4 * j + r] = r < nch ? acc[r] : 0.f;
