@@ -483,7 +483,9 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             wcols += 16 * ((d.grid[gi].ncell + 15) / 16);
         }
         // Rows of an odd number of 16-byte chunks: each lane clears its own row with 16-byte
-        // stores, which then fall in distinct LDS banks.
+        // stores, which then fall in distinct LDS banks. Only the task columns are read (and
+        // so cleared), not the padding.
+        d.wclear = wcols / 8;
         if (wcols % 16 == 0)
             wcols += 8;
         d.wcols = wcols;

@@ -138,6 +138,7 @@ struct Train16Desc {
     int tiles_x, ntiles, nwg, xcd_per; // xcd_per > 0: workgroups of one XCD take consecutive tiles
     int group_off, group_bytes, tile_bytes; // per 4-wave group: target tile, then the union
     int wcols;                              // halves per scatter-weight row (one row per sample)
+    int wclear;                             // 16-byte chunks of a row the reduction reads
     int box_lds_off, box_floats;            // LDS region of the per-sample scatter boxes (bytes, floats)
     int gather_grids;                       // grids with slot_off >= 0
     // NT_SAMPLES_RANDOM: positions at uniformly random texels of the image; no target tile

@@ -1208,11 +1208,12 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         {
             _Float16 *rhi = whi + col * d.wcols, *rlo = wlo + col * d.wcols;
             {
-                // The sample's two weight rows are cleared whole, one by each lane group
-                // (hi by group 0, lo by group 1): a uniform loop of 16-byte stores, ahead
-                // of the corner stores of both groups in program order.
+                // The sample's two weight rows are cleared (their task columns; the
+                // padding is never read), one by each lane group (hi by group 0, lo by
+                // group 1): a uniform loop of 16-byte stores, ahead of the corner stores of
+                // both groups in program order.
                 uint4 *z = (uint4 *)(g ? rlo : rhi);
-                const int n16 = d.wcols >> 3;
+                const int n16 = d.wclear;
 #pragma unroll 4
                 for (int k = 0; k < n16; ++k)
                     z[k] = make_uint4(0u, 0u, 0u, 0u);
