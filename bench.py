@@ -233,7 +233,7 @@ def train_entry(lib, nt, ev, cfg, steps, warmup, sample_mode=0, blocks=False):
         kernel = "train16_kernel<Shape<16,32,2>,3,2,false> (BC6 block phase on expanded texels)"
     if sample_mode:
         kernel = ("train16_kernel<Shape<32,64,2>,16,2,true>" if cfg == 2
-                  else "train16_kernel<Shape<64,64,3>,16,1,true>")
+                  else "train16_kernel<Shape<64,64,3>,16,2,true>")
     if sample_mode:
         # Random texels: bound by scattered memory traffic, priced at the algorithmic bytes
         # per sample (corner gathers, gradient read-modify-write, the taps' target channels).

@@ -382,7 +382,7 @@ hipError_t launch_prep_weights(int shape, const PrepDesc &d, hipStream_t s);
 int train16_groups(int shape, bool random_texels);
 size_t train16_head_bytes(int shape);
 size_t train16_transpose_bytes(int shape);
-int train16_slots(int shape); // dW tiles per wave
+int train16_slots(int shape); // dW slots per round of the end-of-kernel group handoff
 size_t train16_raw_bytes(int shape); // fp16 weight matrices staged in the prologue
 hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream_t s);
 int train_grad_total(int shape);

@@ -858,6 +858,14 @@ __device__ __forceinline__ void gather_records(const Train16Desc &d, float *sbox
     }
 }
 
+// dW slots per round of the end-of-kernel handoff between the two groups: all of them,
+// except for the 4-grid network (random texels), whose group regions hold two.
+template <class S>
+constexpr int handoff_slots()
+{
+    return S::K0 == 64 ? 2 : T16Layout<S, 1>::slots;
+}
+
 template <class S, int C, int NG, bool RND>
 __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc d)
 {
@@ -1494,27 +1502,33 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     // the owner of the second half of a split dW tile hands it to the owner of the first
     // half through group 0's region. Every wave takes part in every barrier.
     if constexpr (NG == 2) {
+        // In rounds of HS slots (17 floats per slot and thread), as many as group 1's region
+        // holds.
+        constexpr int HS = handoff_slots<S>();
         float *xch = (float *)(smem + d.group_off + d.group_bytes);
-        if (gr == 1) {
 #pragma unroll
-            for (int j = 0; j < LY::slots; ++j)
+        for (int r0 = 0; r0 < LY::slots; r0 += HS) {
+            if (r0 > 0)
+                __syncthreads(); // group 0 has read the previous round
+            if (gr == 1) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    xch[(j * 16 + e) * kTrainThreads + t256] = dwacc[j][e];
+                for (int j = r0; j < r0 + HS && j < LY::slots; ++j) {
 #pragma unroll
-            for (int j = 0; j < LY::slots; ++j)
-                xch[(LY::slots * 16 + j) * kTrainThreads + t256] = dbt[j];
-        }
-        __syncthreads();
-        if (gr == 0) {
+                    for (int e = 0; e < 16; ++e)
+                        xch[((j - r0) * 17 + e) * kTrainThreads + t256] = dwacc[j][e];
+                    xch[((j - r0) * 17 + 16) * kTrainThreads + t256] = dbt[j];
+                }
+            }
+            __syncthreads();
+            if (gr == 0) {
 #pragma unroll
-            for (int j = 0; j < LY::slots; ++j)
+                for (int j = r0; j < r0 + HS && j < LY::slots; ++j) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    dwacc[j][e] += xch[(j * 16 + e) * kTrainThreads + t256];
-#pragma unroll
-            for (int j = 0; j < LY::slots; ++j)
-                dbt[j] += xch[(LY::slots * 16 + j) * kTrainThreads + t256];
+                    for (int e = 0; e < 16; ++e)
+                        dwacc[j][e] += xch[((j - r0) * 17 + e) * kTrainThreads + t256];
+                    dbt[j] += xch[((j - r0) * 17 + 16) * kTrainThreads + t256];
+                }
+            }
         }
     }
     float *xfer = (float *)(smem + d.group_off); // [split tile][17][64 lanes]
@@ -1602,7 +1616,7 @@ static hipError_t launch16(const Train16Desc &d, size_t lds, hipStream_t s)
 int train16_groups(int shape, bool random_texels)
 {
     if (random_texels)
-        return shape == kShapeC2 ? 2 : shape == kShapeC4 ? 1 : 0;
+        return shape == kShapeC2 || shape == kShapeC4 ? 2 : 0;
     return shape == kShapeRef || shape == kShapeC2 ? 2 : shape == kShapeC4 ? 1 : 0;
 }
 
@@ -1624,11 +1638,11 @@ int train16_slots(int shape)
 {
     switch (shape) {
     case kShapeRef:
-        return T16Layout<ShapeRef, 2>::slots;
+        return handoff_slots<ShapeRef>();
     case kShapeC2:
-        return T16Layout<ShapeC2, 2>::slots;
+        return handoff_slots<ShapeC2>();
     case kShapeC4:
-        return T16Layout<ShapeC4, 1>::slots;
+        return handoff_slots<ShapeC4>();
     default:
         return 0;
     }
@@ -1663,7 +1677,7 @@ hipError_t launch_train16(int shape, const Train16Desc &d, size_t lds, hipStream
         return d.random_texels ? launch16<ShapeC2, 16, 2, true>(d, lds, s)
                                : launch16<ShapeC2, 16, 2, false>(d, lds, s);
     case kShapeC4:
-        return d.random_texels ? launch16<ShapeC4, 16, 1, true>(d, lds, s)
+        return d.random_texels ? launch16<ShapeC4, 16, 2, true>(d, lds, s)
                                : launch16<ShapeC4, 16, 1, false>(d, lds, s);
     default:
         return hipErrorInvalidValue;
