@@ -252,6 +252,31 @@ __device__ __forceinline__ int wrap_mod(int v, int n)
     return r < 0 ? r + n : r;
 }
 
+// Block (column, row) of block lb of a level's rectangle, wrapped into the level: the row by
+// a float reciprocal and one correction step (exact for rows below 2^16, which the level's
+// block rows are), the wrap by one compare each way (a rectangle narrower than the level
+// starts at most one block outside it; wrap_mod for anything else).
+__device__ __forceinline__ void bc6_block_of(const Bc6PhaseLevel &g, int lb, int &bx, int &by)
+{
+    int ry = (int)((float)lb * __builtin_amdgcn_rcpf((float)g.nbx));
+    int rx = lb - ry * g.nbx;
+    if (rx < 0) {
+        ry -= 1;
+        rx += g.nbx;
+    } else if (rx >= g.nbx) {
+        ry += 1;
+        rx -= g.nbx;
+    }
+    bx = g.bx0 + rx;
+    by = g.by0 + ry;
+    bx = bx < 0 ? bx + g.nbu : (bx >= g.nbu ? bx - g.nbu : bx);
+    by = by < 0 ? by + g.nbv : (by >= g.nbv ? by - g.nbv : by);
+    if ((unsigned)bx >= (unsigned)g.nbu || (unsigned)by >= (unsigned)g.nbv) {
+        bx = wrap_mod(g.bx0 + rx, g.nbu);
+        by = wrap_mod(g.by0 + ry, g.nbv);
+    }
+}
+
 // A block record's fields a pixel thread needs, all loads issued at once (the partition
 // picks the endpoints afterwards): the four endpoints of every channel, the pixel's index
 // on the segment, the partition and the mode.
@@ -297,9 +322,8 @@ __global__ __launch_bounds__(256) void bc6_expand_kernel(Bc6PhaseDesc d)
     const Bc6PhaseLevel &g = d.level[bc6_phase_level(d, b)];
     // A level's rectangle holds fewer than 2^31 blocks (its texels fit 32-bit offsets).
     const int lb = (int)(b - g.first_block);
-    const int ry = lb / g.nbx;
-    const int bx = wrap_mod(g.bx0 + (lb - ry * g.nbx), g.nbu);
-    const int by = wrap_mod(g.by0 + ry, g.nbv);
+    int bx, by;
+    bc6_block_of(g, lb, bx, by);
     const int pix = (int)(t & 15);
     const int x = 4 * bx + (pix & 3), y = 4 * by + (pix >> 2);
     if (x >= g.w || y >= g.h)
@@ -352,7 +376,8 @@ __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
         }
     }
     // The 16 threads of a block are 16 consecutive lanes of one wave (the launch covers
-    // whole blocks), so every shuffle below stays within the block's lanes.
+    // whole blocks), so every cross-lane sum below stays within the block's lanes, and
+    // a block's lanes leave only together.
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t b = t >> 4;
     if (b >= d.total_blocks)
@@ -360,9 +385,8 @@ __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
     const Bc6PhaseLevel &g = d.level[bc6_phase_level(d, b)];
     // A level's rectangle holds fewer than 2^31 blocks (its texels fit 32-bit offsets).
     const int lb = (int)(b - g.first_block);
-    const int ry = lb / g.nbx;
-    const int bx = wrap_mod(g.bx0 + (lb - ry * g.nbx), g.nbu);
-    const int by = wrap_mod(g.by0 + ry, g.nbv);
+    int bx, by;
+    bc6_block_of(g, lb, bx, by);
     const int pix = (int)(t & 15);
     const int64_t blk = (int64_t)by * g.nbu + bx;
     const int x = 4 * bx + (pix & 3), y = 4 * by + (pix >> 2);
@@ -400,13 +424,21 @@ __global__ __launch_bounds__(256) void bc6_fold_kernel(Bc6PhaseDesc d)
     }
     if (touched)
         grec[4 * C + pix] += dl_dx;
+    // Sums over the block's 16 lanes by DPP within each row of 16: lanes xor 1, xor 2
+    // (quad permutations), then the mirrors of each half row and of the row (after the
+    // first two steps every lane of a quad holds the quad's sum, and each mirror pairs every
+    // lane with one of the other half).
 #pragma unroll
-    for (int m = 8; m > 0; m >>= 1)
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int ch = 0; ch < C; ++ch)
-                de[k][ch] += __shfl_xor(de[k][ch], m, 16);
+        for (int ch = 0; ch < C; ++ch) {
+            float v = de[k][ch];
+            v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+            v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+            v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+            v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+            de[k][ch] = v;
+        }
     if (pix == 0) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
