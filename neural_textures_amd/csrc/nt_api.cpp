@@ -563,6 +563,25 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     }
     if (d.box_floats > 0)
         lds = (size_t)d.box_lds_off + ((size_t)d.box_floats + slot_floats) * 4;
+    // The one-group kernel's gather boxes: every grid's chunk cell box, at most 64 cells
+    // (one wave instruction of 64 float4 per wave), whole wave instructions per buffer.
+    d.gbox_off = d.gbox_bytes = d.gbox_items = 0;
+    if (NG == 1 && !c3 && !random) {
+        int cells = 0;
+        bool all = true;
+        for (int gi = 0; gi < G; ++gi) {
+            d.grid[gi].gcell0 = cells;
+            cells += d.grid[gi].ncell;
+            all = all && d.grid[gi].ncell > 0;
+        }
+        const size_t off = (lds + 1023) & ~(size_t)1023, bytes = (size_t)((4 * cells + 63) / 64) * 1024;
+        if (all && cells > 0 && cells <= 64 && off + 2 * bytes <= kMaxLds) {
+            d.gbox_off = (int)off;
+            d.gbox_bytes = (int)bytes;
+            d.gbox_items = 4 * cells;
+            lds = off + 2 * bytes;
+        }
+    }
     // The second group's region carries its dW accumulators to the first at the end.
     const size_t handoff = (size_t)train16_slots(plan->shape) * 17 * kTrainThreads * 4;
     if (NG == 2 && (size_t)d.group_bytes < handoff) {

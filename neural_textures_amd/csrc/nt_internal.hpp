@@ -115,6 +115,7 @@ struct Grid16 {
     // slot_off -1 (k 0): the box takes per-sample LDS atomics.
     int slot_off, gk;
     int wcol0;              // first column of this grid's cells in the scatter weight rows
+    int gcell0;             // first cell of this grid's chunk cell box in the gather boxes
     float inv_cb_w;
     float rx, ry; // grid texels per image texel
 };
@@ -141,6 +142,12 @@ struct Train16Desc {
     int wclear;                             // 16-byte chunks of a row the reduction reads
     int box_lds_off, box_floats;            // LDS region of the per-sample scatter boxes (bytes, floats)
     int gather_grids;                       // grids with slot_off >= 0
+    // One group with every grid in the reduction: the latent texels of each chunk's cell
+    // boxes (at most 64 cells) are copied into LDS one chunk ahead (two buffers of
+    // gbox_bytes from byte offset gbox_off; gbox_items float4, four per cell, grid by grid
+    // from cell gcell0), and the gather reads its corners there. gbox_off 0: the gather
+    // reads global memory.
+    int gbox_off, gbox_bytes, gbox_items;
     // NT_SAMPLES_RANDOM: positions at uniformly random texels of the image; no target tile
     // (taps read from global memory) and per-sample gradient atomics instead of the
     // chunk-box reduction; tiles of 512 consecutive samples.

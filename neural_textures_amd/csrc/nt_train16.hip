@@ -230,6 +230,25 @@ __device__ __forceinline__ h4 lds_read_tr16(const _Float16 *p)
 // each texture, each wave instruction filling 64 consecutive float4 slots (two tile rows;
 // the 12 padding slots of a row repeat its last texel). No registers are held; the caller
 // waits for vmcnt(0) before the barrier that publishes it.
+// A 16-byte copy from global memory into LDS (at the wave-uniform dst + 16 lane) issued
+// from inline assembly, so that the compiler does not track it as an LDS write: it then
+// adds no wait for all outstanding memory operations before the next LDS read (it cannot
+// tell LDS buffers apart), and the kernel waits for these copies itself (vmcnt) before any
+// read of what they write. One wait state separates the M0 write from the copy. M0 is
+// declared clobbered (clang warns that it is a reserved register): the kernels that use
+// this copy set M0 nowhere else.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_untracked(const void *src, void *dst)
+{
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <bool UNTRACKED = false>
 __device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *tile, int cx0, int cy0,
                                                  int wave, int lane)
 {
@@ -244,10 +263,14 @@ __device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *t
         // Unrolled over the (at most four) textures so that their pointers stay in SGPRs.
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-            if (t < d.ntex)
-                __builtin_amdgcn_global_load_lds((const void *)(d.tex[t] + off),
-                                                 (__attribute__((address_space(3))) void *)(tile + t * kT16TileSlots + base),
-                                                 16, 0, 0);
+            if (t < d.ntex) {
+                if constexpr (UNTRACKED)
+                    dma16_untracked((const void *)(d.tex[t] + off), (void *)(tile + t * kT16TileSlots + base));
+                else
+                    __builtin_amdgcn_global_load_lds((const void *)(d.tex[t] + off),
+                                                     (__attribute__((address_space(3))) void *)(tile + t * kT16TileSlots + base),
+                                                     16, 0, 0);
+            }
     }
 }
 
@@ -553,6 +576,112 @@ __device__ __forceinline__ void gather16(const Train16Desc &d, float u, float v,
             x[2 * (j0 + jj)] = lo;
             x[2 * (j0 + jj) + 1] = hi;
         }
+    }
+}
+
+// The latent texels of a chunk's cell boxes (grid by grid, cb_w x cb_h cells from the box
+// origin floor(c0 r - 1/2) that the scatter uses, wrapped into the grid) are copied into an
+// LDS buffer without passing through registers: four float4 per cell, at most 64 cells, so
+// one wave instruction per wave, lane l of wave w copying float4 64 w + l. What does not
+// change from chunk to chunk is set once per launch: the lane's grid and its fields, and
+// its cell's place in the box.
+struct GboxLane {
+    const float *vals; // the grid's mip 0, plus the float4's four floats within the texel
+    float rx, ry;
+    int w, h, cx, cy;
+    bool on;           // the lane has a float4 to copy
+};
+
+template <int G>
+__device__ __forceinline__ GboxLane gbox_lane(const Train16Desc &d, int wave, int lane)
+{
+    GboxLane q;
+    const int i = 64 * wave + lane, cell = i >> 2;
+    q.on = i < d.gbox_items;
+    int gi = 0;
+#pragma unroll
+    for (int k = 1; k < G; ++k)
+        gi += cell >= d.grid[k].gcell0 ? 1 : 0;
+    const Grid16 &g = d.grid[gi];
+    const int local = cell - g.gcell0, cbw = g.cb_w > 0 ? g.cb_w : 1;
+    q.cy = local / cbw;
+    q.cx = local - q.cy * cbw;
+    q.vals = g.values + 4 * (i & 3);
+    q.rx = g.rx;
+    q.ry = g.ry;
+    q.w = g.w;
+    q.h = g.h;
+    return q;
+}
+
+__device__ __forceinline__ void gbox_fetch_async(const GboxLane &q, float4 *buf, int cx0, int cy0, int wave)
+{
+    if (q.on) {
+        int tx = (int)floorf(fmaf((float)cx0, q.rx, -0.5f)) + q.cx;
+        int ty = (int)floorf(fmaf((float)cy0, q.ry, -0.5f)) + q.cy;
+        tx = (unsigned)tx < (unsigned)q.w ? tx : wrap_coord(tx, q.w);
+        ty = (unsigned)ty < (unsigned)q.h ? ty : wrap_coord(ty, q.h);
+        dma16_untracked((const void *)(q.vals + (uint32_t)(ty * q.w + tx) * 16u), (void *)(buf + 64 * wave));
+    }
+}
+
+// gather16 with the corners read from the chunk's gather boxes in LDS: the same values,
+// products and fp16 sums. A wave with a footprint outside its grid's box (not expected: the
+// box covers every corner a chunk position can reach) reads global memory instead.
+template <int G>
+__device__ __forceinline__ void gather16_box(const Train16Desc &d, const float4 *box, const Grid16 (&own)[G / 2],
+                                             int cx0, int cy0, float u, float v, int g, h8 (&x)[G])
+{
+    constexpr int J = G / 2;
+    Footprint f[J];
+    int a[J];
+    bool in = true;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int cbw = own[j].cb_w;
+        f[j] = bilinear_footprint(u, v, own[j].w, own[j].h, 1.f);
+        const int lx = f[j].x0 - (int)floorf(fmaf((float)cx0, own[j].rx, -0.5f));
+        const int ly = f[j].y0 - (int)floorf(fmaf((float)cy0, own[j].ry, -0.5f));
+        in = in && lx >= 0 && lx + 1 < cbw && ly >= 0 && ly + 1 < own[j].cb_h;
+        a[j] = 4 * (own[j].gcell0 + ly * cbw + lx);
+    }
+    if (__ballot(!in) != 0) {
+        gather16<G, true>(d, u, v, g, x);
+        return;
+    }
+    typedef float nf4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) const nf4 lds_nf4;
+    lds_nf4 *lb = (lds_nf4 *)box;
+    // Grid pair by grid pair: the next pair's 16 reads are issued before this pair's
+    // products, so that their latency overlaps them.
+    float4 t[J][4][4];
+    auto load = [&](int j) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int o = a[j] + ((c >> 1) ? 4 * own[j].cb_w : 0) + ((c & 1) ? 4 : 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                t[j][c][k] = __builtin_bit_cast(float4, lb[o + k]);
+        }
+    };
+    load(0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        if (j + 1 < J) {
+            // This pair's data first (s_waitcnt lgkmcnt(0), which the compiler's own wait
+            // placement then counts), then the next pair's reads, kept ahead of the products.
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            load(j + 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        h8 lo = (h8)(_Float16)0.f, hi = (h8)(_Float16)0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            lo = accumulate_products(lo, f[j].w[c], t[j][c][0], t[j][c][1]);
+            hi = accumulate_products(hi, f[j].w[c], t[j][c][2], t[j][c][3]);
+        }
+        x[2 * j] = lo;
+        x[2 * j + 1] = hi;
     }
 }
 
@@ -897,6 +1026,29 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
     _Float16 *whi = un + kChunk * dx_stride(S::K0); // scatter weights [sample][wcols], hi
     _Float16 *wlo = whi + kChunk * d.wcols;     // ... lo
 
+    // The tile of the workgroup's k-th turn (k = b0 / gridDim.x) and its origin.
+    auto tile_origin = [&](int b0, int &tx0, int &ty0) {
+        int b = b0;
+        if (d.xcd_per > 0)
+            b = (b & 7) * d.xcd_per + (b >> 3); // the workgroups of one XCD share an L2: give them neighbouring tiles
+        tx0 = (b % d.tiles_x) * (kChunkW * 4);
+        ty0 = (b / d.tiles_x) * (kChunkH * NG);
+        return b;
+    };
+    // Gather boxes (one group): the first chunk's now, each later chunk's during the chunk
+    // before it (two buffers).
+    constexpr bool GBOX = PF && !RND && C == 16;
+    float4 *gbox = (float4 *)(smem + d.gbox_off);
+    const int gbox_step = d.gbox_bytes / 16;
+    GboxLane gl{};
+    if constexpr (GBOX) {
+        if (d.gbox_off != 0) {
+            gl = gbox_lane<G>(d, wave, lane);
+            int fx0, fy0;
+            tile_origin(blockIdx.x, fx0, fy0);
+            gbox_fetch_async(gl, gbox, d.off_x + fx0, d.off_y + fy0, wave);
+        }
+    }
     {
         // Weight image (staged through the group regions, which the tile loop overwrites only
         // after the barriers below) and biases.
@@ -906,6 +1058,8 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         __syncthreads();
         for (int f = __builtin_amdgcn_readfirstlane(tid >> 6); f < S::all_frags(); f += NT / kWave)
             frags[f * kWave + lane] = weight_fragment16<S, C>(raw, d.perm, f, lane);
+        if constexpr (GBOX)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the first gather boxes
         __syncthreads();
     }
 
@@ -942,6 +1096,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         own[j].cb_h = g ? sreg(qb.cb_h) : sreg(qa.cb_h);
         own[j].ncell = g ? sreg(qb.ncell) : sreg(qa.ncell);
         own[j].wcol0 = g ? sreg(qb.wcol0) : sreg(qa.wcol0);
+        own[j].gcell0 = g ? sreg(qb.gcell0) : sreg(qa.gcell0);
         own[j].rx = g ? sreg(qb.rx) : sreg(qa.rx);
         own[j].ry = g ? sreg(qb.ry) : sreg(qa.ry);
         own[j].grads = g ? sreg(qb.grads) : sreg(qa.grads);
@@ -1005,11 +1160,10 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 
     // Tiles of the region, several per workgroup when there are more tiles than workgroups;
     // the MLP gradient accumulates over all of them.
+    int gq = 0; // chunks done: the gather-box buffer of this one is gq & 1
     for (int b0 = blockIdx.x; b0 < d.ntiles; b0 += gridDim.x) {
-    int b = b0;
-    if (d.xcd_per > 0)
-        b = (b & 7) * d.xcd_per + (b >> 3); // the workgroups of one XCD share an L2: give them neighbouring tiles
-    const int tx0 = (b % d.tiles_x) * (kChunkW * 4), ty0 = (b / d.tiles_x) * (kChunkH * NG);
+    int tx0, ty0;
+    const int b = tile_origin(b0, tx0, ty0);
     // Scatter boxes (the 3-channel network's fine grids; the planner places none for 16
     // channels): cleared here (the previous tile's flush ended with a barrier, and the
     // chunk's barriers order this before the first add); box origin of the lane's grids.
@@ -1026,8 +1180,13 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 
     for (int chunk = 0; chunk < 4; ++chunk) {
         const int cx0 = d.off_x + tx0 + chunk * kChunkW, cy0 = d.off_y + ty0 + kChunkH * gr;
-        if constexpr (!RND)
+        // With gather boxes both copies are untracked: the gather's LDS reads (another buffer)
+        // then wait for neither.
+        if constexpr (GBOX)
+            tile_fetch_async<true>(d, tile, cx0, cy0, wave, lane);
+        else if constexpr (!RND)
             tile_fetch_async(d, tile, cx0, cy0, wave, lane);
+        const float4 *gcur = gbox + (gq & 1) * gbox_step;
 
         // ---- sample position (train.cu:827-844)
         const int sx = tx0 + chunk * kChunkW + (c & 15);
@@ -1059,7 +1218,12 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 
         h8 x0[KQ0];
         if (valid) {
-            if constexpr (C == 16)
+            if constexpr (GBOX) {
+                if (d.gbox_off != 0)
+                    gather16_box<G>(d, gcur, own, cx0, cy0, u, v, g, x0);
+                else
+                    gather16<G, PF>(d, u, v, g, x0);
+            } else if constexpr (C == 16)
                 gather16<G, PF>(d, u, v, g, x0);
             else
                 gather3(d, u, v, g, x0);
@@ -1067,6 +1231,22 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
 #pragma unroll
             for (int q = 0; q < KQ0; ++q)
                 x0[q] = (h8)(_Float16)0.f;
+        }
+
+        // The next chunk's gather boxes (this tile's next chunk or the next tile's first),
+        // issued once this chunk's gather is done; complete with the target tile at the
+        // barrier before the targets.
+        if constexpr (GBOX) {
+            if (d.gbox_off != 0) {
+                float4 *gnext = gbox + ((gq + 1) & 1) * gbox_step;
+                if (chunk < 3) {
+                    gbox_fetch_async(gl, gnext, cx0 + kChunkW, cy0, wave);
+                } else if (b0 + (int)gridDim.x < d.ntiles) {
+                    int nx0, ny0;
+                    tile_origin(b0 + gridDim.x, nx0, ny0);
+                    gbox_fetch_async(gl, gnext, d.off_x + nx0, d.off_y + ny0, wave);
+                }
+            }
         }
 
         // ---- forward (mlp.h:65-99)
@@ -1468,6 +1648,7 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         }
         } // region scatter
         // The next chunk writes the union only after its first barrier.
+        ++gq;
     }
 
     // Flush the tile's scatter boxes: grid by grid, the non-zero sums added to the

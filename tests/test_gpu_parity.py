@@ -240,8 +240,9 @@ def test_train_step_several_tiles_per_workgroup(lib, O, shape):
 def test_train_step_scatter_out_of_box_paths(lib, O, shape):
     """Without the margin of the chunk cell box, many footprints fall outside it: the
     scatter adds those per sample with atomics (the 16-channel kernel to global memory, the
-    general kernel of the 3-channel network into its LDS footprint box). Gradients still
-    match the oracle's."""
+    general kernel of the 3-channel network into its LDS footprint box), and the one-group
+    kernel's gather reads those waves' corners from global memory instead of its LDS copy
+    of the cell boxes. Gradients still match the oracle's."""
     say(f"case: train {shape} without box margins")
     nt.check(lib.nt_set_test_hooks(0, 1))
     try:
