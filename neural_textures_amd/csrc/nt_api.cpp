@@ -1766,7 +1766,8 @@ static bool plan_decode_box(const nt_decode_params *p, const FwdDesc &fd, int sh
                 bh = std::max(bh, box_last(y1, p->out_height, p->jitter, h) -
                                       box_origin(y0, p->out_height, p->jitter, h) + 2);
             }
-            if (bw > 0xFFFF || bh > 0x7FFF || (int64_t)bw * bh * 32 > kBoxMaxBytes)
+            // The kernel packs a mip's dimensions into 16 bits each.
+            if (bw > 0xFFFF || bh > 0x7FFF || (int64_t)bw * bh * 32 > kBoxMaxBytes || w > 0xFFFF || h > 0xFFFF)
                 return false;
             q.box_w[m] = bw;
             q.box_h[m] = bh;

@@ -562,7 +562,12 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
     h8 *frags = (h8 *)smem;
     float *bias = (float *)(smem + LY::bias_off);
     uint4 *box = (uint4 *)(smem + d.lds_box_off);
+    // The (grid, mip) entry of every box texel, after the boxes: the boxes' places do not
+    // change from block to block, so it is found once per launch.
+    uint8_t *owner = (uint8_t *)(box + 2 * d.box_texels);
     __shared__ int4 tab[NT_MAX_GRIDS * NT_MAX_MIPS];
+    // Per (grid, mip): the mip's dimensions (w | h << 16), 1/box width, the mip's texels.
+    __shared__ int4 tab2[NT_MAX_GRIDS * NT_MAX_MIPS];
     __shared__ BoxSample samp[NT_MAX_GRIDS * NT_MAX_MIPS];
     __shared__ int max_mip[NT_MAX_GRIDS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 31, g = lane >> 5;
@@ -571,6 +576,16 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
     stage_weights<S, true, true>(d.mlp, frags, bias, tid, kFwdThreads);
     if (tid < NT_MAX_GRIDS)
         max_mip[tid] = tid < d.G && d.grid[tid].num_mips > 0 ? d.grid[tid].num_mips - 1 : 0;
+    for (int k = tid; k < d.box_texels; k += kFwdThreads) {
+        int o = 0;
+        for (int a = 0; a < d.G; ++a) {
+            const BoxGrid &q = d.grid[a];
+            for (int b = q.mip_lo; b <= q.mip_hi; ++b)
+                if (k >= q.box_off[b])
+                    o = a * NT_MAX_MIPS + b;
+        }
+        owner[k] = (uint8_t)o;
+    }
 
     const int nblocks = d.blocks_x * d.blocks_y;
     for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
@@ -590,32 +605,46 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
             }
             tab[tid] = e;
             const int bw = e.y & 0xFFFF;
+            if (gi < d.G) {
+                const BoxGrid &q = d.grid[gi];
+                const uintptr_t base = (uintptr_t)(q.texels + q.mip_off[m] * 16);
+                tab2[tid] = make_int4(mip_dim(q.w, m) | (mip_dim(q.h, m) << 16), __float_as_int(1.f / (float)bw),
+                                      (int)(uint32_t)base, (int)(uint32_t)(base >> 32));
+            }
             samp[tid] = BoxSample{box_addr + 32 * (e.x - e.w * bw - e.z), 32 * bw,
                                   gi < d.G ? (float)mip_dim(d.grid[gi].w, m) : 1.f,
                                   gi < d.G ? (float)mip_dim(d.grid[gi].h, m) : 1.f};
         }
         __syncthreads();
         // Stage the boxes: texel k of box (gi, m) is global texel (origin + (k % bw, k / bw)),
-        // wrapped; two 16-byte halves per texel.
+        // wrapped; two 16-byte halves per texel, copied into LDS without passing through
+        // registers (lane l of a wave instruction writes the l-th 16 bytes from its base).
+        // k / bw by a float reciprocal and one correction (below 2^22).
         for (int i = tid; i < 2 * d.box_texels; i += kFwdThreads) {
-            const int k = i >> 1;
-            int gi = 0, m = 0;
-            for (int a = 0; a < d.G; ++a) {
-                const BoxGrid &q = d.grid[a];
-                for (int b = q.mip_lo; b <= q.mip_hi; ++b)
-                    if (k >= q.box_off[b]) {
-                        gi = a;
-                        m = b;
-                    }
-            }
-            const BoxGrid &q = d.grid[gi];
-            const int4 e = tab[gi * NT_MAX_MIPS + m];
+            const int k = i >> 1, o = owner[k];
+            const int4 e = tab[o], f = tab2[o];
             const int bw = e.y & 0xFFFF, local = k - e.x;
-            const int w = mip_dim(q.w, m), h = mip_dim(q.h, m);
-            const int gx = wrap_mod(e.z + local % bw, w), gy = wrap_mod(e.w + local / bw, h);
-            const uint4 *src = (const uint4 *)(q.texels + (q.mip_off[m] + (int64_t)gy * w + gx) * 16);
-            box[i] = load_global(src + (i & 1));
+            int ly = (int)((float)local * __int_as_float(f.y));
+            int lx = local - ly * bw;
+            if (lx >= bw) {
+                lx -= bw;
+                ++ly;
+            } else if (lx < 0) {
+                lx += bw;
+                --ly;
+            }
+            const int w = f.x & 0xFFFF, h = (int)((uint32_t)f.x >> 16);
+            int gx = e.z + lx, gy = e.w + ly;
+            if ((unsigned)gx >= (unsigned)w)
+                gx = wrap_mod(gx, w);
+            if ((unsigned)gy >= (unsigned)h)
+                gy = wrap_mod(gy, h);
+            const uint16_t *base = (const uint16_t *)(((uintptr_t)(uint32_t)f.w << 32) | (uint32_t)f.z);
+            const uint4 *src = (const uint4 *)(base + ((int64_t)gy * w + gx) * 16) + (i & 1);
+            __builtin_amdgcn_global_load_lds((const void *)src,
+                                             (__attribute__((address_space(3))) void *)(box + (i & ~63)), 16, 0, 0);
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
 
         // Two tiles per wave at a time (t and t + kFwdWaves), sharing the weight reads.
@@ -710,7 +739,7 @@ static hipError_t launch_box(const DecodeBoxDesc &d, hipStream_t s)
 {
     const int nblocks = d.blocks_x * d.blocks_y;
     const int grid = nblocks < 2048 ? nblocks : 2048;
-    const size_t lds = (size_t)d.lds_box_off + (size_t)d.box_texels * 32;
+    const size_t lds = (size_t)d.lds_box_off + (size_t)d.box_texels * 33; // the boxes and their owner bytes
     if ((size_t)d.lds_box_off < FwdLayout<S>::bytes)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(decode_box_kernel<S>, dim3(grid), dim3(kFwdThreads), lds, s, d);
