@@ -566,7 +566,8 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
     // change from block to block, so it is found once per launch.
     uint8_t *owner = (uint8_t *)(box + 2 * d.box_texels);
     __shared__ int4 tab[NT_MAX_GRIDS * NT_MAX_MIPS];
-    // Per (grid, mip): the mip's dimensions (w | h << 16), 1/box width, the mip's texels.
+    // Per (grid, mip): the mip's dimensions (w | h << 16), 1/box width (0: no box), the
+    // mip's texels.
     __shared__ int4 tab2[NT_MAX_GRIDS * NT_MAX_MIPS];
     __shared__ BoxSample samp[NT_MAX_GRIDS * NT_MAX_MIPS];
     __shared__ int max_mip[NT_MAX_GRIDS];
@@ -576,6 +577,24 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
     stage_weights<S, true, true>(d.mlp, frags, bias, tid, kFwdThreads);
     if (tid < NT_MAX_GRIDS)
         max_mip[tid] = tid < d.G && d.grid[tid].num_mips > 0 ? d.grid[tid].num_mips - 1 : 0;
+    // Per (grid, mip), once per launch: the box's place and size (tab.xy; the origins, tab.zw,
+    // are each block's), and tab2 (mip dimensions, 1/box width, or 0 with no box, texels).
+    if (tid < NT_MAX_GRIDS * NT_MAX_MIPS) {
+        const int gi = tid / NT_MAX_MIPS, m = tid % NT_MAX_MIPS;
+        int4 e = make_int4(0, 0x20002, 0, 0), f = make_int4(0, 0, 0, 0);
+        if (gi < d.G) {
+            const BoxGrid &q = d.grid[gi];
+            const uintptr_t base = (uintptr_t)(q.texels + q.mip_off[m] * 16);
+            f = make_int4(mip_dim(q.w, m) | (mip_dim(q.h, m) << 16), 0, (int)(uint32_t)base, (int)(uint32_t)(base >> 32));
+            if (m >= q.mip_lo && m <= q.mip_hi) {
+                e.x = q.box_off[m];
+                e.y = q.box_w[m] | (q.box_h[m] << 16);
+                f.y = __float_as_int(1.f / (float)q.box_w[m]);
+            }
+        }
+        tab[tid] = e;
+        tab2[tid] = f;
+    }
     for (int k = tid; k < d.box_texels; k += kFwdThreads) {
         int o = 0;
         for (int a = 0; a < d.G; ++a) {
@@ -592,28 +611,18 @@ __global__ __launch_bounds__(kFwdThreads, 4) void decode_box_kernel(DecodeBoxDes
         const int bx0 = (blk % d.blocks_x) * kBoxBlockW, by0 = (blk / d.blocks_x) * kBoxBlockH;
         __syncthreads(); // the previous block's reads of the boxes (and the weight staging) are done
         if (tid < NT_MAX_GRIDS * NT_MAX_MIPS) {
-            const int gi = tid / NT_MAX_MIPS, m = tid % NT_MAX_MIPS;
-            int4 e = make_int4(0, 0x20002, 0, 0);
-            if (gi < d.G) {
-                const BoxGrid &q = d.grid[gi];
-                if (m >= q.mip_lo && m <= q.mip_hi) {
-                    e.x = q.box_off[m];
-                    e.y = q.box_w[m] | (q.box_h[m] << 16);
-                    e.z = box_origin(bx0, d.image_w, d.jitter, mip_dim(q.w, m));
-                    e.w = box_origin(by0, d.image_h, d.jitter, mip_dim(q.h, m));
-                }
+            // The block's box origins, from the launch's table (LDS).
+            int4 e = tab[tid];
+            const int4 f = tab2[tid];
+            const int mw = f.x & 0xFFFF, mh = (int)((uint32_t)f.x >> 16);
+            if (f.y != 0) {
+                e.z = box_origin(bx0, d.image_w, d.jitter, mw);
+                e.w = box_origin(by0, d.image_h, d.jitter, mh);
+                tab[tid] = e;
             }
-            tab[tid] = e;
             const int bw = e.y & 0xFFFF;
-            if (gi < d.G) {
-                const BoxGrid &q = d.grid[gi];
-                const uintptr_t base = (uintptr_t)(q.texels + q.mip_off[m] * 16);
-                tab2[tid] = make_int4(mip_dim(q.w, m) | (mip_dim(q.h, m) << 16), __float_as_int(1.f / (float)bw),
-                                      (int)(uint32_t)base, (int)(uint32_t)(base >> 32));
-            }
-            samp[tid] = BoxSample{box_addr + 32 * (e.x - e.w * bw - e.z), 32 * bw,
-                                  gi < d.G ? (float)mip_dim(d.grid[gi].w, m) : 1.f,
-                                  gi < d.G ? (float)mip_dim(d.grid[gi].h, m) : 1.f};
+            samp[tid] = BoxSample{box_addr + 32 * (e.x - e.w * bw - e.z), 32 * bw, f.x != 0 ? (float)mw : 1.f,
+                                  f.x != 0 ? (float)mh : 1.f};
         }
         __syncthreads();
         // Stage the boxes: texel k of box (gi, m) is global texel (origin + (k % bw, k / bw)),
