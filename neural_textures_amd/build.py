@@ -10,6 +10,8 @@ Every HIP source is compiled for gfx950 only, with:
                                      more than 256 registers otherwise get their MFMA
                                      results in AGPRs and copy every one out before the VALU
                                      can use it (v_accvgpr_read)
+nt_train16.hip is compiled a second time (UNITS["random"]) for its random-texel kernels
+alone, with -amdgpu-sched-strategy=max-memory-clause.
 """
 from __future__ import annotations
 
@@ -23,8 +25,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libnt_hip.so")
-SOURCES = ["nt_api.cpp", "nt_train.hip", "nt_train16.hip", "nt_forward.hip", "nt_adam.hip", "nt_codec.hip",
-           "nt_bc6.hip", "nt_model.cpp"]
+SOURCES = ["nt_api.cpp", "nt_train.hip", "nt_train16.hip", "nt_train16.hip:random", "nt_forward.hip", "nt_adam.hip",
+           "nt_codec.hip", "nt_bc6.hip", "nt_model.cpp"]
+# Objects built from a source a second time ("file:unit"): their defines and extra flags.
+UNITS = {
+    "random": ["-DNT_TRAIN16_RANDOM_UNIT", "-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
+}
 HOST_DIR = os.path.join(HERE, "host")
 HOST_SOURCES = ["nt_host.cpp", "nt_train_main.cpp"]
 HOST_PROGRAM = os.path.join(HOST_DIR, "nt_train")
@@ -46,11 +52,13 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(entry: str) -> str:
+    src, _, unit = entry.partition(":")
+    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + (f"_{unit}" if unit else "") + ".o")
+    extra = UNITS[unit] if unit else []
+    cmd = [HIPCC, *FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
-        cmd = [HIPCC, "-x", "hip", *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [HIPCC, "-x", "hip", *FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")

@@ -387,6 +387,8 @@ hipError_t launch_prep_weights(int shape, const PrepDesc &d, hipStream_t s);
 // 16-channel kernel: groups of four waves per workgroup (1 or 2) for this shape, the
 // static LDS bytes (weights), the transposes' bytes, and the launchers.
 int train16_groups(int shape, bool random_texels);
+// The random-texel kernels (nt_train16.hip compiled with NT_TRAIN16_RANDOM_UNIT).
+hipError_t launch_train16_random(int shape, const Train16Desc &d, size_t lds, hipStream_t s);
 size_t train16_head_bytes(int shape);
 size_t train16_transpose_bytes(int shape);
 int train16_slots(int shape); // dW slots per round of the end-of-kernel group handoff
