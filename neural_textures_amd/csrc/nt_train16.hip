@@ -234,19 +234,20 @@ __device__ __forceinline__ h4 lds_read_tr16(const _Float16 *p)
 // from inline assembly, so that the compiler does not track it as an LDS write: it then
 // adds no wait for all outstanding memory operations before the next LDS read (it cannot
 // tell LDS buffers apart), and the kernel waits for these copies itself (vmcnt) before any
-// read of what they write. One wait state separates the M0 write from the copy. M0 is
-// declared clobbered (clang warns that it is a reserved register): the kernels that use
-// this copy set M0 nowhere else.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
+// read of what they write. M0 (the copy's LDS address) is saved and restored around it,
+// so the compiler's own use of M0 is undisturbed; one wait state separates the M0 write
+// from the copy, and one the copy from the restore.
 __device__ __forceinline__ void dma16_untracked(const void *src, void *dst)
 {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)dst);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0)
-                 : "memory", "m0");
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+                 "s_nop 0\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(src), "s"(m0)
+                 : "memory");
 }
-#pragma clang diagnostic pop
 
 template <bool UNTRACKED = false>
 __device__ __forceinline__ void tile_fetch_async(const Train16Desc &d, float4 *tile, int cx0, int cy0,
