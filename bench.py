@@ -44,19 +44,19 @@ FLOP_PER_FORWARD_C1 = 9600           # 2 x (8*64 + 64*64 + 64*3)
 # HBM bytes per train-kernel launch: rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 (KiB),
 # the factors being what the two counters read for a 256 MiB device copy (--copy-probe).
 # Counters cannot be read live; re-measured whenever the kernel changes.
-TRAIN_HBM_BYTES_PER_LAUNCH = {0: (7096.5 * 2.0 + 4181.4) * 1024,
-                              2: (7668.3 * 2.0 + 11470.0) * 1024,
-                              4: (28934.6 * 2.0 + 37302.1) * 1024,
-                              10: (9158.7 * 2.0 + 8478.5) * 1024}
+TRAIN_HBM_BYTES_PER_LAUNCH = {0: (7102.0 * 2.0 + 4181.4) * 1024,
+                              2: (7669.1 * 2.0 + 11470.0) * 1024,
+                              4: (29020.1 * 2.0 + 37302.6) * 1024,
+                              10: (9164.4 * 2.0 + 8478.5) * 1024}
 # Random-texel steps: algorithmic bytes per sample = corner gathers (grids x 4 x 64 B) +
 # gradient read-modify-write (2 x that) + the targets' channels at 16 taps x 4 B.
 RANDOM_BYTES_PER_SAMPLE = {2: 2 * 4 * 64 * 3 + 16 * 9 * 4,    # 2,112
                            4: 4 * 4 * 64 * 3 + 16 * 12 * 4}   # 3,840
-TRAIN_HBM_BYTES_RANDOM = {2: (347000.0 * 2.0 + 138384.0) * 1024,    # same counters, config 2 random texels
-                          4: (1772986.8 * 2.0 + 1182484.4) * 1024}  # and config 4 random texels
+TRAIN_HBM_BYTES_RANDOM = {2: (348243.4 * 2.0 + 138384.0) * 1024,    # same counters, config 2 random texels
+                          4: (1773730.8 * 2.0 + 1182998.4) * 1024}  # and config 4 random texels
 # The BC6 block phase's train kernel (the reference network on texels expanded from its
 # BCf-2k block records), same counters.
-TRAIN_HBM_BYTES_BC6 = (9164.1 * 2.0 + 8478.2) * 1024
+TRAIN_HBM_BYTES_BC6 = (9164.0 * 2.0 + 8478.2) * 1024
 WORKLOADS = ("c4", "c2", "c2r", "c4r", "c5", "c3", "c1", "cref", "cref2k", "crefbc6")
 
 
