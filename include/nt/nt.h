@@ -260,10 +260,15 @@ int nt_profile_next_launch(void *start_event, void *stop_event);
  * runs). Process-wide, taking effect at the next nt_train_step:
  *   max_train_workgroups > 0 caps the 16-channel train kernel's workgroups (0: one per
  *   compute unit), so that small regions give each workgroup several tiles;
- *   drop_scatter_margins != 0 removes the margin of that kernel's chunk cell box, which
- *   drives its latent scatter's out-of-box path (per-sample global atomics).
+ *   flags bit 0 (NT_HOOK_DROP_MARGINS) removes the margin of that kernel's chunk cell box,
+ *   which drives its latent scatter's out-of-box path (per-sample global atomics);
+ *   flags bit 1 (NT_HOOK_SORT_RANDOM) makes NT_SAMPLES_RANDOM steps sort their samples by
+ *   bin at any sample count (they do from a million samples), so that small tests reach
+ *   the sorted order.
  * nt_set_test_hooks(0, 0) restores the defaults. */
-int nt_set_test_hooks(int max_train_workgroups, int drop_scatter_margins);
+#define NT_HOOK_DROP_MARGINS 1
+#define NT_HOOK_SORT_RANDOM 2
+int nt_set_test_hooks(int max_train_workgroups, int flags);
 
 /* ---- the hot path ----------------------------------------------------------------- */
 

@@ -45,6 +45,10 @@ NT_LATENT_TOUCHED = 1
 NT_FILTER_BILINEAR = 0
 NT_FILTER_CATMULL_ROM = 1
 
+# nt_set_test_hooks flags
+NT_HOOK_DROP_MARGINS = 1
+NT_HOOK_SORT_RANDOM = 2
+
 f32p = C.POINTER(C.c_float)
 u16p = C.POINTER(C.c_uint16)
 

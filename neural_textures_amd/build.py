@@ -26,7 +26,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libnt_hip.so")
 SOURCES = ["nt_api.cpp", "nt_train.hip", "nt_train16.hip", "nt_train16.hip:random", "nt_forward.hip", "nt_adam.hip",
-           "nt_codec.hip", "nt_bc6.hip", "nt_model.cpp"]
+           "nt_codec.hip", "nt_bc6.hip", "nt_sort.hip", "nt_model.cpp"]
 # Objects built from a source a second time ("file:unit"): their defines and extra flags.
 UNITS = {
     "random": ["-DNT_TRAIN16_RANDOM_UNIT", "-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],

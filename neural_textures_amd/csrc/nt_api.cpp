@@ -24,6 +24,7 @@ thread_local char g_error[512] = "";
 // Test hooks (nt_set_test_hooks): process-wide, read once per train step plan.
 std::atomic<int> g_hook_max_workgroups{0};
 std::atomic<int> g_hook_no_margins{0};
+std::atomic<int> g_hook_sort_random{0};
 thread_local hipEvent_t g_prof_start = nullptr;
 thread_local hipEvent_t g_prof_stop = nullptr;
 
@@ -333,6 +334,10 @@ struct TrainPlan {
     // The 16-channel unconstrained kernel (nt_train16.hip), when it applies.
     int use16, groups, rows;
     Train16Desc t16;
+    // Its random-texel sample order (nt_sort.hip): byte offset of the sort buffers in the
+    // workspace (0: no sort), the bins a row and the key bits, the temporary storage.
+    size_t sort_off, sort_temp;
+    int sort_bins_x, sort_key_bits, sort_shift;
     // The BC6 block phase (Bc6PhaseDesc): the rest of the plan is the inner unconstrained
     // step's. Per grid the mips the inner step sees (its chain stops after the last level a
     // sample reaches) and the workspace offsets of the expanded chain and its gradients; per
@@ -601,6 +606,37 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->rows = d.nwg; // the groups of a workgroup merge their partials in LDS
     plan->weight_bytes = 0; // each workgroup builds its weight image in LDS
     plan->workspace = (size_t)plan->rows * (size_t)plan->P * sizeof(float);
+    // Random texels: the sort of the sample indices by bin after the partial rows (keys and
+    // values double-buffered, then the sort's temporary storage). Its size comes from the
+    // device's sort configuration; without a device (a plan made for its sizes only) a bound
+    // that the run-time query is checked against. The sort (the binning kernel and hipCUB's
+    // radix sort: six launches, ~70-85 us) pays for itself from about a million samples:
+    // config 4 with random texels (1,048,576) runs its train kernel 1,392 -> 1,120 us with
+    // it, config 2 (262,144) only 204 -> 176 us.
+    plan->sort_off = plan->sort_temp = 0;
+    if (random && (p->num_samples >= kRandomSortMinSamples || g_hook_sort_random.load(std::memory_order_relaxed))) {
+        // Bins of 64 x 64 texels (coarser ones, one 8-bit sort pass, gained less).
+        const int shift = 6;
+        const int bx = (p->image_width + (1 << shift) - 1) >> shift;
+        const int by = (p->image_height + (1 << shift) - 1) >> shift;
+        plan->sort_shift = shift;
+        if ((int64_t)bx * by <= 65536) {
+            int bits = 1;
+            while ((1 << bits) < bx * by)
+                ++bits;
+            const size_t n = (size_t)p->num_samples;
+            size_t temp = 0;
+            if (random_order_temp_bytes(p->num_samples, bits, &temp) != hipSuccess || temp == 0)
+                temp = std::max((size_t)1 << 20, n * 8);
+            temp = (temp + 255) & ~(size_t)255;
+            const size_t keys = (n * 2 + 255) & ~(size_t)255, vals = (n * 4 + 255) & ~(size_t)255;
+            plan->sort_off = (plan->workspace + 255) & ~(size_t)255;
+            plan->sort_temp = temp;
+            plan->sort_bins_x = bx;
+            plan->sort_key_bits = bits;
+            plan->workspace = plan->sort_off + 2 * keys + 2 * vals + temp;
+        }
+    }
     d.image_w = p->image_width;
     d.image_h = p->image_height;
     d.off_x = p->texel_offset_x;
@@ -918,12 +954,15 @@ const char *nt_status_string(int status)
 
 const char *nt_last_error(void) { return g_error; }
 
-int nt_set_test_hooks(int max_train_workgroups, int drop_scatter_margins)
+int nt_set_test_hooks(int max_train_workgroups, int flags)
 {
     if (max_train_workgroups < 0)
         return fail(NT_ERR_INVALID_ARGUMENT, "max_train_workgroups %d", max_train_workgroups);
+    if (flags & ~(NT_HOOK_DROP_MARGINS | NT_HOOK_SORT_RANDOM))
+        return fail(NT_ERR_INVALID_ARGUMENT, "test hook flags %d", flags);
     g_hook_max_workgroups.store(max_train_workgroups, std::memory_order_relaxed);
-    g_hook_no_margins.store(drop_scatter_margins ? 1 : 0, std::memory_order_relaxed);
+    g_hook_no_margins.store(flags & NT_HOOK_DROP_MARGINS ? 1 : 0, std::memory_order_relaxed);
+    g_hook_sort_random.store(flags & NT_HOOK_SORT_RANDOM ? 1 : 0, std::memory_order_relaxed);
     return ok();
 }
 
@@ -1092,6 +1131,29 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
                 continue;
             }
             footprint_rect(p, p->latents.grids[gi].width, p->latents.grids[gi].height, d.rect[gi]);
+        }
+        if (plan.sort_off) {
+            // NT_SAMPLES_RANDOM: the slots' samples sorted by bin.
+            const size_t n = (size_t)p->num_samples;
+            const size_t keys = (n * 2 + 255) & ~(size_t)255, vals = (n * 4 + 255) & ~(size_t)255;
+            uint8_t *b = ws + plan.sort_off;
+            RandomOrderDesc r{};
+            r.n = p->num_samples;
+            r.step = (uint32_t)p->step;
+            r.image_w = p->image_width;
+            r.image_h = p->image_height;
+            r.bins_x = plan.sort_bins_x;
+            r.key_bits = plan.sort_key_bits;
+            r.bin_shift = plan.sort_shift;
+            r.keys = (uint16_t *)b;
+            r.keys_alt = (uint16_t *)(b + keys);
+            r.vals = (uint32_t *)(b + 2 * keys);
+            r.vals_alt = (uint32_t *)(b + 2 * keys + vals);
+            r.temp = b + 2 * keys + 2 * vals;
+            r.temp_bytes = plan.sort_temp;
+            e = launch_random_order(r, s, &d.order);
+            if (e != hipSuccess)
+                return hip_status(e, "random-texel sample order");
         }
         {
             ProfileScope prof(s);

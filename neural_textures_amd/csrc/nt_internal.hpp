@@ -120,6 +120,23 @@ struct Grid16 {
     float rx, ry; // grid texels per image texel
 };
 
+// NT_SAMPLES_RANDOM: the sample indices sorted by the 64 x 64-texel bin of their texels
+// (nt_sort.hip). Keys and values in two buffers each (the radix sort's double buffers) and
+// the sort's temporary storage, all in the train workspace.
+constexpr int kRandomSortMinSamples = 1 << 20; // fewer samples train in slot order
+struct RandomOrderDesc {
+    int n;
+    uint32_t step;
+    int image_w, image_h, bins_x, key_bits, bin_shift;
+    uint16_t *keys, *keys_alt;
+    uint32_t *vals, *vals_alt;
+    void *temp;
+    size_t temp_bytes;
+};
+hipError_t random_order_temp_bytes(int n, int key_bits, size_t *bytes);
+// Bins, then the stable sort; *order is the sorted sample indices (one of the value buffers).
+hipError_t launch_random_order(const RandomOrderDesc &d, hipStream_t s, const uint32_t **order);
+
 struct Train16Desc {
     Grid16 grid[NT_MAX_GRIDS];
     const float *tex[4]; // reference textures (pitch 4, image size), output rows 4t .. 4t+3
@@ -152,6 +169,7 @@ struct Train16Desc {
     // (taps read from global memory) and per-sample gradient atomics instead of the
     // chunk-box reduction; tiles of 512 consecutive samples.
     int random_texels;
+    const uint32_t *order; // random texels: the sample of each slot (NULL: slot i is sample i)
     uint64_t perm;                          // nibble r: output index of output row r
     MlpDesc mlp;                            // fp16 weights and biases, read in the prologue
     float *partial; // [nwg][grad_total]

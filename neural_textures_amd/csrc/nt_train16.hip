@@ -996,7 +996,7 @@ constexpr int handoff_slots()
     return S::K0 == 64 ? 2 : T16Layout<S, 1>::slots;
 }
 
-template <class S, int C, int NG, bool RND>
+template <class S, int C, int NG, bool RND, bool ORD = false>
 __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc d)
 {
     static_assert(!RND || C == 16, "random texels are built for 16-channel grids");
@@ -1195,10 +1195,15 @@ __global__ __launch_bounds__(kTrainThreads *NG) void train16_kernel(Train16Desc 
         uint32_t sidx = (uint32_t)sy * (uint32_t)d.region_w + (uint32_t)sx;
         bool valid = sx < d.region_w && sidx < (uint32_t)d.num_samples;
         if constexpr (RND) {
-            // Sample 512 (NG b + gr) + 128 chunk + 32 wave + c: tiles of consecutive samples.
+            // Slot 512 (NG b + gr) + 128 chunk + 32 wave + c: tiles of consecutive slots; with
+            // ORD each holds the sample the bin-sorted order gives it, else slot i is sample i.
             sidx = (((((uint32_t)b * NG + (uint32_t)gr) * 4u + (uint32_t)chunk) * 4u + (uint32_t)wave) * 32u) +
                    (uint32_t)c;
             valid = sidx < (uint32_t)d.num_samples;
+            if constexpr (ORD) {
+                if (valid)
+                    sidx = d.order[sidx];
+            }
         }
         uint32_t st = mix_seed(sidx, d.step);
         uint32_t tx = (uint32_t)(d.off_x + sx), ty = (uint32_t)(d.off_y + sy);
@@ -1779,10 +1784,10 @@ using ShapeRef = Shape<16, 32, 2>;
 using ShapeC2 = Shape<32, 64, 2>;
 using ShapeC4 = Shape<64, 64, 3>;
 
-template <class S, int C, int NG, bool RND>
+template <class S, int C, int NG, bool RND, bool ORD = false>
 static hipError_t launch16(const Train16Desc &d, size_t lds, hipStream_t s)
 {
-    auto k = train16_kernel<S, C, NG, RND>;
+    auto k = train16_kernel<S, C, NG, RND, ORD>;
     // Raise the kernel's dynamic LDS limit to the whole 160 KB once (thread-safe).
     static std::once_flag once;
     static hipError_t configured = hipSuccess;
@@ -1806,9 +1811,9 @@ hipError_t launch_train16_random(int shape, const Train16Desc &d, size_t lds, hi
 {
     switch (shape) {
     case kShapeC2:
-        return launch16<ShapeC2, 16, 2, true>(d, lds, s);
+        return d.order ? launch16<ShapeC2, 16, 2, true, true>(d, lds, s) : launch16<ShapeC2, 16, 2, true>(d, lds, s);
     case kShapeC4:
-        return launch16<ShapeC4, 16, 2, true>(d, lds, s);
+        return d.order ? launch16<ShapeC4, 16, 2, true, true>(d, lds, s) : launch16<ShapeC4, 16, 2, true>(d, lds, s);
     default:
         return hipErrorInvalidValue;
     }

@@ -244,7 +244,7 @@ def test_train_step_scatter_out_of_box_paths(lib, O, shape):
     kernel's gather reads those waves' corners from global memory instead of its LDS copy
     of the cell boxes. Gradients still match the oracle's."""
     say(f"case: train {shape} without box margins")
-    nt.check(lib.nt_set_test_hooks(0, 1))
+    nt.check(lib.nt_set_test_hooks(0, abi.NT_HOOK_DROP_MARGINS))
     try:
         st, gs, alt = run_train_pair(lib, O, shape, 128, (64, 32), (11, 21), abi.NT_UNCONSTRAINED)
     finally:
@@ -252,24 +252,57 @@ def test_train_step_scatter_out_of_box_paths(lib, O, shape):
     check_train_grads(st, gs, alt, biases=False)
 
 
-@pytest.mark.parametrize("shape,region,max_wg", [("ref", (64, 32), 0), ("c1", (64, 32), 0), ("c2", (64, 32), 0),
-                                                 ("c4", (64, 32), 0), ("c2", (50, 13), 2), ("c4", (100, 7), 1),
-                                                 ("c2", (100, 30), 2)],
-                         ids=["ref", "c1", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg", "c2-3tiles-2wg"])
-def test_train_step_random_texels(lib, O, shape, region, max_wg):
+@pytest.mark.parametrize("shape,region,max_wg,flags", [
+    ("ref", (64, 32), 0, 0), ("c1", (64, 32), 0, 0), ("c2", (64, 32), 0, 0), ("c4", (64, 32), 0, 0),
+    ("c2", (50, 13), 2, 0), ("c4", (100, 7), 1, 0), ("c2", (100, 30), 2, 0),
+    # the 16-channel kernel's slots in bin order (a step sorts from a million samples)
+    ("c2", (64, 32), 0, abi.NT_HOOK_SORT_RANDOM), ("c4", (100, 7), 1, abi.NT_HOOK_SORT_RANDOM),
+    ("c2", (100, 30), 2, abi.NT_HOOK_SORT_RANDOM),
+], ids=["ref", "c1", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg", "c2-3tiles-2wg", "c2-sorted",
+        "c4-ragged-1wg-sorted", "c2-3tiles-2wg-sorted"])
+def test_train_step_random_texels(lib, O, shape, region, max_wg, flags):
     """NT_SAMPLES_RANDOM: samples anywhere in the image (the 16-channel kernel with taps
     from global memory and per-sample corner atomics; the general kernel for the reference
     network); gradients match the oracle's at the MLP tolerance. Ragged regions leave
     partial tiles; one or two workgroups walk every tile (config 2 runs two groups of 512
-    samples per tile: 3,000 samples are three tiles, two of them on one workgroup)."""
-    say(f"case: train {shape} random texels region {region} max workgroups {max_wg}")
-    nt.check(lib.nt_set_test_hooks(max_wg, 0))
+    samples per tile: 3,000 samples are three tiles, two of them on one workgroup). With the
+    samples sorted by bin the kernel's slots hold other samples, placed as before: the same
+    gradients."""
+    say(f"case: train {shape} random texels region {region} max workgroups {max_wg} flags {flags}")
+    nt.check(lib.nt_set_test_hooks(max_wg, flags))
     try:
         st, gs, alt = run_train_pair(lib, O, shape, 128, region, (0, 0), abi.NT_UNCONSTRAINED, seed=17,
                                      sample_mode=abi.NT_SAMPLES_RANDOM)
     finally:
         nt.check(lib.nt_set_test_hooks(0, 0))
     check_train_grads(st, gs, alt)
+
+
+def test_random_texel_sorted_step_is_deterministic(lib):
+    """The bin sort of NT_SAMPLES_RANDOM is stable, so a step's slots hold the same samples
+    on every run and the network gradient (summed per workgroup in slot order, then in a
+    fixed order) is bit-identical across runs; the latent gradients (float atomics) match
+    to rounding."""
+    import torch
+    say("case: random texels sorted, two runs")
+    st = make_state("c2", image=256, region=(128, 64), seed=23)
+    st.sample_mode = abi.NT_SAMPLES_RANDOM
+    nt.check(lib.nt_set_test_hooks(0, abi.NT_HOOK_SORT_RANDOM))
+    try:
+        runs = []
+        for _ in range(2):
+            g = gpu_workspace(lib, st.to_torch(), abi.NT_UNCONSTRAINED)
+            nt.check(lib.nt_train_step(C.byref(g.params()), abi.NT_UNCONSTRAINED, None))
+            sync()
+            runs.append(g)
+    finally:
+        nt.check(lib.nt_set_test_hooks(0, 0))
+    a, b = runs
+    for x, y in zip((*a.net.weight_grads, *a.net.bias_grads), (*b.net.weight_grads, *b.net.bias_grads)):
+        assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+    assert torch.count_nonzero(a.net.weight_grads[0]) > 0
+    for ga, gb in zip(a.grids, b.grids):
+        assert_close(to_np(gb.grads), to_np(ga.grads), "latent grads of two runs", tol=1e-5, floor=1e-6)
 
 
 def test_train_step_accumulates(lib, O):
@@ -761,21 +794,25 @@ def _run_iterations(lib, a, b, ktype, offs):
         yield i
 
 
-@pytest.mark.parametrize("shape,mode,update,ktype,blocks,image,region", [
-    ("c2", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32)),
-    ("c4", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_UNCONSTRAINED, False, 128, (64, 32)),
-    ("c2", abi.NT_SAMPLES_RANDOM, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32)),
-    ("ref", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_UNCONSTRAINED, False, 128, (64, 32)),
-    ("ref", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_BLOCK_FEATURES, True, 128, (64, 32)),
-    ("ref16", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32)),
-    ("ref16f", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_UNCONSTRAINED, False, 128, (64, 32)),
+@pytest.mark.parametrize("shape,mode,update,ktype,blocks,image,region,flags", [
+    ("c2", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32), 0),
+    ("c4", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_UNCONSTRAINED, False, 128, (64, 32), 0),
+    ("c2", abi.NT_SAMPLES_RANDOM, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32), 0),
+    ("ref", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_UNCONSTRAINED, False, 128, (64, 32), 0),
+    ("ref", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_BLOCK_FEATURES, True, 128, (64, 32), 0),
+    ("ref16", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32), 0),
+    ("ref16f", abi.NT_SAMPLES_REGION, abi.NT_LATENT_DENSE, abi.NT_UNCONSTRAINED, False, 128, (64, 32), 0),
     # more partial rows than reduction ranges (one row per train workgroup: 128 for c2,
     # one per CU for c4), so a different split of the rows would change the sums' bits
-    ("c2", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 512, (512, 256)),
-    ("c4", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 512, (512, 256)),
+    ("c2", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 512, (512, 256), 0),
+    ("c4", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 512, (512, 256), 0),
+    # random texels in bin order (a step sorts from a million samples): the same sort on both
+    # paths, so the same slots
+    ("c2", abi.NT_SAMPLES_RANDOM, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32),
+     abi.NT_HOOK_SORT_RANDOM),
 ], ids=["c2-touched", "c4-dense", "c2-random-touched", "ref", "ref-blocks", "ref16-touched", "ref16f-dense",
-        "c2-many-rows", "c4-many-rows"])
-def test_train_iteration_equals_three_calls(lib, shape, mode, update, ktype, blocks, image, region):
+        "c2-many-rows", "c4-many-rows", "c2-random-sorted"])
+def test_train_iteration_equals_three_calls(lib, shape, mode, update, ktype, blocks, image, region, flags):
     """nt_train_iteration (the train step with the MLP-gradient reduction and both
     optimizers in one launch) against nt_train_step + nt_optimize_network +
     nt_optimize_latents, over four iterations with moving regions and a decaying feature
@@ -788,34 +825,39 @@ def test_train_iteration_equals_three_calls(lib, shape, mode, update, ktype, blo
     same inputs (a last-bit latent difference can flip an fp16 feature rounding and with it
     the next step's network gradient)."""
     import torch
-    say(f"case: train iteration {shape} mode {mode} update {update} type {ktype} image {image} region {region}")
-    st = make_state(shape, image=image, region=region, seed=9, blocks=blocks)
-    st.sample_mode = mode
-    st.latent_update = update
-    a = gpu_workspace(lib, st.to_torch(), ktype)
-    b = gpu_workspace(lib, st.to_torch(), ktype)
-    # Past the first iteration the latents of the two paths differ by the order of their
-    # float atomics, which at 131,072 samples flips fp16 feature roundings and with them
-    # every later gradient; the large cases therefore check the one iteration whose inputs
-    # are identical on both paths.
-    n_iter = 4 if image <= 128 else 1
-    offs = np.random.default_rng(5).integers(0, max(image - region[0], 1), size=(n_iter, 2))
-    for i in _run_iterations(lib, a, b, ktype, offs):
-        bb = dict(_all_buffers(b))
-        for name, x in _all_buffers(a):
-            y = bb[name]
-            if name.startswith("grid"):
-                xf, yf = x.float(), y.float()
-                scale = max(float(yf.abs().max()), 1e-30)
-                assert float((xf - yf).abs().max()) <= 1e-5 * scale, f"iteration {i}: {name}"
-                if "grads" in name:
-                    assert torch.count_nonzero(x) == 0 and torch.count_nonzero(y) == 0, f"iteration {i}: {name}"
-            else:
-                assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), f"iteration {i}: {name}"
-        for name, x in _all_buffers(a):
-            if name.startswith("grid"):
-                bb[name].copy_(x)
-        sync()
+    say(f"case: train iteration {shape} mode {mode} update {update} type {ktype} image {image} region {region} "
+        f"flags {flags}")
+    nt.check(lib.nt_set_test_hooks(0, flags))  # before the workspaces are sized
+    try:
+        st = make_state(shape, image=image, region=region, seed=9, blocks=blocks)
+        st.sample_mode = mode
+        st.latent_update = update
+        a = gpu_workspace(lib, st.to_torch(), ktype)
+        b = gpu_workspace(lib, st.to_torch(), ktype)
+        # Past the first iteration the latents of the two paths differ by the order of their
+        # float atomics, which at 131,072 samples flips fp16 feature roundings and with them
+        # every later gradient; the large cases therefore check the one iteration whose inputs
+        # are identical on both paths.
+        n_iter = 4 if image <= 128 else 1
+        offs = np.random.default_rng(5).integers(0, max(image - region[0], 1), size=(n_iter, 2))
+        for i in _run_iterations(lib, a, b, ktype, offs):
+            bb = dict(_all_buffers(b))
+            for name, x in _all_buffers(a):
+                y = bb[name]
+                if name.startswith("grid"):
+                    xf, yf = x.float(), y.float()
+                    scale = max(float(yf.abs().max()), 1e-30)
+                    assert float((xf - yf).abs().max()) <= 1e-5 * scale, f"iteration {i}: {name}"
+                    if "grads" in name:
+                        assert torch.count_nonzero(x) == 0 and torch.count_nonzero(y) == 0, f"iteration {i}: {name}"
+                else:
+                    assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), f"iteration {i}: {name}"
+            for name, x in _all_buffers(a):
+                if name.startswith("grid"):
+                    bb[name].copy_(x)
+            sync()
+    finally:
+        nt.check(lib.nt_set_test_hooks(0, 0))
     assert torch.count_nonzero(a.net.weight_moment1[0]) > 0
 
 
