@@ -247,7 +247,9 @@ int64_t nt_mip_chain_layout(int width, int height, int num_mips, int64_t *mip_of
 /* The same for 4x4 block storage (blocks per dimension = max(size>>2, 1), train.cu:220). */
 int64_t nt_block_chain_layout(int width, int height, int num_mips, int64_t *block_offset);
 /* Bytes of scratch nt_train_step needs for these parameters (0 on error); also enough for
- * nt_inference's fixed-order SSE. */
+ * nt_inference's fixed-order SSE. A NT_SAMPLES_RANDOM step of a million samples or more also
+ * holds its sample sort, sized for the current device (without one, a bound that the step
+ * checks against the device's own size). */
 size_t nt_train_workspace_bytes(const nt_params *params, nt_kernel_type type);
 
 /* Profiling hook (no reference counterpart): the next nt_train_step, nt_optimize_latents,
