@@ -53,7 +53,7 @@ TRAIN_HBM_BYTES_PER_LAUNCH = {0: (7102.0 * 2.0 + 4181.4) * 1024,
 RANDOM_BYTES_PER_SAMPLE = {2: 2 * 4 * 64 * 3 + 16 * 9 * 4,    # 2,112
                            4: 4 * 4 * 64 * 3 + 16 * 12 * 4}   # 3,840
 TRAIN_HBM_BYTES_RANDOM = {2: (348243.4 * 2.0 + 138384.0) * 1024,    # same counters, config 2 random texels
-                          4: (1773730.8 * 2.0 + 1182998.4) * 1024}  # and config 4 random texels
+                          4: (886018.2 * 2.0 + 1183507.0) * 1024}   # and config 4 random texels (bin-sorted)
 # The BC6 block phase's train kernel (the reference network on texels expanded from its
 # BCf-2k block records), same counters.
 TRAIN_HBM_BYTES_BC6 = (9164.0 * 2.0 + 8478.2) * 1024
