@@ -225,15 +225,15 @@ def train_entry(lib, nt, ev, cfg, steps, warmup, sample_mode=0, blocks=False):
     n = st.num_samples
     flops = FLOP_PER_TRAIN_SAMPLE[cfg] * n
     achieved = flops / (kmean / 1e3) / 1e12
-    kernel = {0: "train16_kernel<Shape<16,32,2>,3,2,false>", 10: "train16_kernel<Shape<16,32,2>,3,2,false>",
-              2: "train16_kernel<Shape<32,64,2>,16,2,false>",
-              4: "train16_kernel<Shape<64,64,3>,16,1,false>"}[cfg]
+    kernel = {0: "train16_kernel<Shape<16,32,2>,3,2,false,false>", 10: "train16_kernel<Shape<16,32,2>,3,2,false,false>",
+              2: "train16_kernel<Shape<32,64,2>,16,2,false,false>",
+              4: "train16_kernel<Shape<64,64,3>,16,1,false,false>"}[cfg]
     if blocks:
         # The block phase: records expanded to texels, this kernel, gradients folded back.
-        kernel = "train16_kernel<Shape<16,32,2>,3,2,false> (BC6 block phase on expanded texels)"
+        kernel = "train16_kernel<Shape<16,32,2>,3,2,false,false> (BC6 block phase on expanded texels)"
     if sample_mode:
-        kernel = ("train16_kernel<Shape<32,64,2>,16,2,true>" if cfg == 2
-                  else "train16_kernel<Shape<64,64,3>,16,2,true>")
+        kernel = ("train16_kernel<Shape<32,64,2>,16,2,true,false>" if cfg == 2
+                  else "train16_kernel<Shape<64,64,3>,16,2,true,true>")
     if sample_mode:
         # Random texels: bound by scattered memory traffic, priced at the algorithmic bytes
         # per sample (corner gathers, gradient read-modify-write, the taps' target channels).
