@@ -252,15 +252,20 @@ def test_train_step_scatter_out_of_box_paths(lib, O, shape):
     check_train_grads(st, gs, alt, biases=False)
 
 
-@pytest.mark.parametrize("shape,region,max_wg,flags", [
-    ("ref", (64, 32), 0, 0), ("c1", (64, 32), 0, 0), ("c2", (64, 32), 0, 0), ("c4", (64, 32), 0, 0),
-    ("c2", (50, 13), 2, 0), ("c4", (100, 7), 1, 0), ("c2", (100, 30), 2, 0),
+@pytest.mark.parametrize("shape,region,max_wg,flags,image", [
+    ("ref", (64, 32), 0, 0, 128), ("c1", (64, 32), 0, 0, 128), ("c2", (64, 32), 0, 0, 128),
+    ("c4", (64, 32), 0, 0, 128), ("c2", (50, 13), 2, 0, 128), ("c4", (100, 7), 1, 0, 128),
+    ("c2", (100, 30), 2, 0, 128),
     # the 16-channel kernel's slots in bin order (a step sorts from a million samples)
-    ("c2", (64, 32), 0, abi.NT_HOOK_SORT_RANDOM), ("c4", (100, 7), 1, abi.NT_HOOK_SORT_RANDOM),
-    ("c2", (100, 30), 2, abi.NT_HOOK_SORT_RANDOM),
+    ("c2", (64, 32), 0, abi.NT_HOOK_SORT_RANDOM, 128), ("c4", (100, 7), 1, abi.NT_HOOK_SORT_RANDOM, 128),
+    ("c2", (100, 30), 2, abi.NT_HOOK_SORT_RANDOM, 128),
+    # images that are no multiple of the 64-texel bins: partial bins on the right and bottom
+    ("c2", (64, 32), 0, 0, 168), ("c2", (64, 32), 0, abi.NT_HOOK_SORT_RANDOM, 168),
+    ("c4", (100, 7), 1, abi.NT_HOOK_SORT_RANDOM, 200),
 ], ids=["ref", "c1", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg", "c2-3tiles-2wg", "c2-sorted",
-        "c4-ragged-1wg-sorted", "c2-3tiles-2wg-sorted"])
-def test_train_step_random_texels(lib, O, shape, region, max_wg, flags):
+        "c4-ragged-1wg-sorted", "c2-3tiles-2wg-sorted", "c2-image168", "c2-image168-sorted",
+        "c4-image200-1wg-sorted"])
+def test_train_step_random_texels(lib, O, shape, region, max_wg, flags, image):
     """NT_SAMPLES_RANDOM: samples anywhere in the image (the 16-channel kernel with taps
     from global memory and per-sample corner atomics; the general kernel for the reference
     network); gradients match the oracle's at the MLP tolerance. Ragged regions leave
@@ -268,10 +273,10 @@ def test_train_step_random_texels(lib, O, shape, region, max_wg, flags):
     samples per tile: 3,000 samples are three tiles, two of them on one workgroup). With the
     samples sorted by bin the kernel's slots hold other samples, placed as before: the same
     gradients."""
-    say(f"case: train {shape} random texels region {region} max workgroups {max_wg} flags {flags}")
+    say(f"case: train {shape} random texels image {image} region {region} max workgroups {max_wg} flags {flags}")
     nt.check(lib.nt_set_test_hooks(max_wg, flags))
     try:
-        st, gs, alt = run_train_pair(lib, O, shape, 128, region, (0, 0), abi.NT_UNCONSTRAINED, seed=17,
+        st, gs, alt = run_train_pair(lib, O, shape, image, region, (0, 0), abi.NT_UNCONSTRAINED, seed=17,
                                      sample_mode=abi.NT_SAMPLES_RANDOM)
     finally:
         nt.check(lib.nt_set_test_hooks(0, 0))
