@@ -335,7 +335,7 @@ struct TrainPlan {
     int use16, groups, rows;
     Train16Desc t16;
     // Its random-texel sample order (nt_sort.hip): byte offset of the sort buffers in the
-    // workspace (0: no sort), the bins a row and the key bits, the temporary storage.
+    // workspace (0: no sort), the bins a row and the key bits, the digit counts' bytes.
     size_t sort_off, sort_temp;
     int sort_bins_x, sort_key_bits, sort_shift;
     // The BC6 block phase (Bc6PhaseDesc): the rest of the plan is the inner unconstrained
@@ -607,12 +607,9 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
     plan->weight_bytes = 0; // each workgroup builds its weight image in LDS
     plan->workspace = (size_t)plan->rows * (size_t)plan->P * sizeof(float);
     // Random texels: the sort of the sample indices by bin after the partial rows (keys and
-    // values double-buffered, then the sort's temporary storage). Its size comes from the
-    // device's sort configuration; without a device (a plan made for its sizes only) a bound
-    // that the run-time query is checked against. The sort (the binning kernel and hipCUB's
-    // radix sort: six launches, ~70-85 us) pays for itself from about a million samples:
-    // config 4 with random texels (1,048,576) runs its train kernel 1,392 -> 1,120 us with
-    // it, config 2 (262,144) only 204 -> 176 us.
+    // sample indices in two buffers each, then the per-tile digit counts). From 262,144
+    // samples: config 2 with random texels runs its train kernel 204 -> 176 us with it,
+    // config 4 (1,048,576 samples) 1,392 -> 1,120 us.
     plan->sort_off = plan->sort_temp = 0;
     if (random && (p->num_samples >= kRandomSortMinSamples || g_hook_sort_random.load(std::memory_order_relaxed))) {
         // Bins of 64 x 64 texels (coarser ones, one 8-bit sort pass, gained less).
@@ -625,10 +622,7 @@ void plan16(const nt_params *p, nt_kernel_type type, TrainPlan *plan)
             while ((1 << bits) < bx * by)
                 ++bits;
             const size_t n = (size_t)p->num_samples;
-            size_t temp = 0;
-            if (random_order_temp_bytes(p->num_samples, bits, &temp) != hipSuccess || temp == 0)
-                temp = std::max((size_t)1 << 20, n * 8);
-            temp = (temp + 255) & ~(size_t)255;
+            const size_t temp = (random_order_count_bytes(p->num_samples, bits) + 255) & ~(size_t)255;
             const size_t keys = (n * 2 + 255) & ~(size_t)255, vals = (n * 4 + 255) & ~(size_t)255;
             plan->sort_off = (plan->workspace + 255) & ~(size_t)255;
             plan->sort_temp = temp;
@@ -1145,12 +1139,13 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
             r.bins_x = plan.sort_bins_x;
             r.key_bits = plan.sort_key_bits;
             r.bin_shift = plan.sort_shift;
+            random_order_tiles(r.n, &r.tile, &r.tiles);
+            r.high_bits = random_order_high_bits(r.key_bits, r.tiles);
             r.keys = (uint16_t *)b;
             r.keys_alt = (uint16_t *)(b + keys);
             r.vals = (uint32_t *)(b + 2 * keys);
             r.vals_alt = (uint32_t *)(b + 2 * keys + vals);
-            r.temp = b + 2 * keys + 2 * vals;
-            r.temp_bytes = plan.sort_temp;
+            r.counts = (uint32_t *)(b + 2 * keys + 2 * vals);
             e = launch_random_order(r, s, &d.order);
             if (e != hipSuccess)
                 return hip_status(e, "random-texel sample order");

@@ -121,20 +121,29 @@ struct Grid16 {
 };
 
 // NT_SAMPLES_RANDOM: the sample indices sorted by the 64 x 64-texel bin of their texels
-// (nt_sort.hip). Keys and values in two buffers each (the radix sort's double buffers) and
-// the sort's temporary storage, all in the train workspace.
-constexpr int kRandomSortMinSamples = 1 << 20; // fewer samples train in slot order
+// (nt_sort.hip). Keys and sample indices in two buffers each (the counting sort's two passes)
+// and the per-tile digit counts, all in the train workspace.
+constexpr int kRandomSortMinSamples = 1 << 18; // fewer samples train in slot order
+constexpr int kRandomSortTile = 4096;          // samples per workgroup in the counting passes
+constexpr int kRandomSortMaxTiles = 256;       // more samples make the tiles longer
 struct RandomOrderDesc {
     int n;
     uint32_t step;
     int image_w, image_h, bins_x, key_bits, bin_shift;
+    int high_bits; // random_order_high_bits: key_bits (one pass), else 8 (the first pass's digit)
+    int tile;      // samples per tile: kRandomSortTile, or more for over 256 tiles
+    int tiles;     // ceil(n / tile), at most kRandomSortMaxTiles
     uint16_t *keys, *keys_alt;
     uint32_t *vals, *vals_alt;
-    void *temp;
-    size_t temp_bytes;
+    uint32_t *counts; // (1 << high_bits) x tiles
 };
-hipError_t random_order_temp_bytes(int n, int key_bits, size_t *bytes);
-// Bins, then the stable sort; *order is the sorted sample indices (one of the value buffers).
+// The tiles of the counting passes for n samples.
+void random_order_tiles(int n, int *tile, int *tiles);
+// The first pass's digit bits: key_bits when one pass sorts the keys, else 8.
+int random_order_high_bits(int key_bits, int tiles);
+// Bytes of the per-tile digit counts for n samples and keys of key_bits bits.
+size_t random_order_count_bytes(int n, int key_bits);
+// Bins, then the stable sort; *order is the sorted sample indices (d.vals).
 hipError_t launch_random_order(const RandomOrderDesc &d, hipStream_t s, const uint32_t **order);
 
 struct Train16Desc {

@@ -262,9 +262,11 @@ def test_train_step_scatter_out_of_box_paths(lib, O, shape):
     # images that are no multiple of the 64-texel bins: partial bins on the right and bottom
     ("c2", (64, 32), 0, 0, 168), ("c2", (64, 32), 0, abi.NT_HOOK_SORT_RANDOM, 168),
     ("c4", (100, 7), 1, abi.NT_HOOK_SORT_RANDOM, 200),
+    # several tiles of the one-pass sort; keys of 11 bits (33 x 33 bins): the two-pass sort
+    ("c2", (128, 100), 0, abi.NT_HOOK_SORT_RANDOM, 128), ("c2", (100, 100), 0, abi.NT_HOOK_SORT_RANDOM, 2112),
 ], ids=["ref", "c1", "c2", "c4", "c2-ragged-2wg", "c4-ragged-1wg", "c2-3tiles-2wg", "c2-sorted",
         "c4-ragged-1wg-sorted", "c2-3tiles-2wg-sorted", "c2-image168", "c2-image168-sorted",
-        "c4-image200-1wg-sorted"])
+        "c4-image200-1wg-sorted", "c2-4tiles-sorted", "c2-image2112-two-pass-sorted"])
 def test_train_step_random_texels(lib, O, shape, region, max_wg, flags, image):
     """NT_SAMPLES_RANDOM: samples anywhere in the image (the 16-channel kernel with taps
     from global memory and per-sample corner atomics; the general kernel for the reference
