@@ -135,7 +135,8 @@ struct RandomOrderDesc {
     int tiles;     // ceil(n / tile), at most kRandomSortMaxTiles
     uint16_t *keys, *keys_alt;
     uint32_t *vals, *vals_alt;
-    uint32_t *counts; // (1 << high_bits) x tiles
+    uint32_t *counts; // tiles x max(4, 1 << high_bits), then the segment starts
+    uint32_t *seg;    // (1 << high_bits) + 1 segment starts (set by launch_random_order)
 };
 // The tiles of the counting passes for n samples.
 void random_order_tiles(int n, int *tile, int *tiles);

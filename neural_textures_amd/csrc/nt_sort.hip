@@ -7,24 +7,18 @@
 // only the order of the fp32 sums moves. A stable sort by key has one result, so the order is
 // the same on every run.
 //
-// Keys of at most ten bits (config 2's 1,024 bins) take two launches: sort_count_kernel
-// (below) with its counts tile-major, then sort_one_pass_kernel, where each workgroup
-// derives its digits' places from all tiles' counts (the digit totals scanned, plus its
-// digit's counts in earlier tiles) and places its tile's samples as in launch 3 below.
-// Longer keys: a most-significant-digit counting sort in four launches, all integer work:
-//   1. sort_count_kernel: each workgroup takes a tile of consecutive samples (4,096, or
-//      more so that there are at most 256 tiles), computes their bin keys (stored for the
-//      later passes) and counts the tile's keys per high digit (the top eight key bits) in
-//      LDS;
-//   2. sort_scan_kernel: one workgroup turns the counts (digit-major: digit h of every tile,
-//      then h + 1) into exclusive offsets, so digit h of tile b starts where every smaller
-//      digit and digit h of every earlier tile end;
-//   3. sort_scatter_kernel: each tile again, in order, 256 samples a round (the keys of 16
-//      rounds loaded at once, so that the rounds wait on no memory); a sample's place
-//      is its digit's running offset + the samples before it in the round with the same digit
-//      (a wave's lanes by ballots on the digit bits, the waves before it by their counts);
-//   4. sort_segment_kernel: one workgroup per high digit sorts that digit's segment by the
-//      low key bits the same way (its counts in LDS), writing the final order.
+// The sort is a counting sort by digits, all integer work. sort_count_kernel: each workgroup
+// takes a tile of consecutive samples (4,096, or more so that there are at most 256 tiles),
+// computes their bin keys (stored for the later passes) and counts them per first digit in
+// LDS (the whole key when it has at most ten bits, config 2's 1,024 bins; else its top eight
+// bits). sort_first_pass_kernel: each workgroup derives where its tile's samples of each
+// digit start from all tiles' counts (the digits' totals, scanned, plus the digit's counts
+// in earlier tiles), then places its samples in order, 256 a round (the keys of 16 rounds
+// loaded at once, so that the rounds wait on no memory): a sample's place is its digit's
+// running place + the samples before it in the round with the same digit (a wave's lanes by
+// ballots on the digit bits, the waves before it by their counts). Keys of more than ten
+// bits then go through sort_segment_kernel: one workgroup per first digit sorts that digit's
+// segment by the remaining key bits the same way, writing the final order.
 #include <hip/hip_runtime.h>
 
 #include "nt_internal.hpp"
@@ -35,7 +29,6 @@ namespace {
 
 constexpr int kSortThreads = 256, kSortWaves = kSortThreads / 64;
 constexpr int kSortRegs = 16;   // items per thread loaded at once in the scatter passes
-constexpr int kScanRegs = 64;   // counts per thread of the scan (at most 256 tiles x 256 digits)
 constexpr int kSortMaxDigits = 1024; // digits of a one-pass sort (keys of at most ten bits)
 
 __device__ __forceinline__ uint32_t bin_key(const RandomOrderDesc &d, uint32_t i)
@@ -91,8 +84,7 @@ __device__ __forceinline__ uint32_t round_place(uint32_t digit, int bits, bool v
     return pos;
 }
 
-// Counts per tile and digit: tile-major rows of max(4, digits) counts for one-pass keys,
-// digit-major rows of the tiles' counts otherwise.
+// Counts per tile and first digit: tile-major rows of max(4, digits) counts.
 __global__ __launch_bounds__(kSortThreads) void sort_count_kernel(RandomOrderDesc d)
 {
     __shared__ uint32_t hist[kSortMaxDigits];
@@ -111,46 +103,58 @@ __global__ __launch_bounds__(kSortThreads) void sort_count_kernel(RandomOrderDes
         }
     }
     __syncthreads();
-    if (low == 0) {
-        const int stride = ndig < 4 ? 4 : ndig;
-        for (int x = t; x < stride; x += kSortThreads)
-            d.counts[(int64_t)blockIdx.x * stride + x] = x < ndig ? hist[x] : 0u;
-    } else if (t < ndig) {
-        d.counts[(int64_t)t * d.tiles + blockIdx.x] = hist[t];
-    }
+    const int stride = ndig < 4 ? 4 : ndig;
+    for (int x = t; x < stride; x += kSortThreads)
+        d.counts[(int64_t)blockIdx.x * stride + x] = x < ndig ? hist[x] : 0u;
 }
 
-// Keys of at most ten bits, sorted whole in this pass (see the top of the file).
-__global__ __launch_bounds__(kSortThreads) void sort_one_pass_kernel(RandomOrderDesc d)
+// base[x] (x < max(4, digits)): where this workgroup's first sample of first digit x goes.
+// Thread t sums digits 4g .. 4g + 3 (g = t mod G, G = max(4, digits) / 4 groups) over the
+// tiles of range t / G (256 / G ranges), 16-byte loads issued 16 at a time; the ranges are
+// added in LDS, then the groups' totals scanned.
+__device__ __forceinline__ void tile_bases(const RandomOrderDesc &d, uint32_t *base, uint32_t (*red)[kSortThreads][4],
+                                           uint32_t *part)
 {
-    __shared__ uint32_t base[kSortMaxDigits];
-    __shared__ uint32_t wcnt[kSortWaves][kSortMaxDigits];
-    __shared__ uint32_t part[kSortThreads];
     const int t = threadIdx.x, tile = blockIdx.x;
-    const int ndig = 1 << d.key_bits, stride = ndig < 4 ? 4 : ndig;
-    // Digits 4t .. 4t + 3: their totals over all tiles and their counts in earlier tiles.
+    const int ndig = 1 << d.high_bits, stride = ndig < 4 ? 4 : ndig;
+    const int groups = stride / 4, ranges = kSortThreads / groups;
+    const int g = t % groups, r = t / groups;
+    const int per = (d.tiles + ranges - 1) / ranges, b_lo = min(r * per, d.tiles), b_hi = min(b_lo + per, d.tiles);
     uint32_t tot[4] = {0u, 0u, 0u, 0u}, pre[4] = {0u, 0u, 0u, 0u};
-    if (4 * t < stride) {
-        for (int b0 = 0; b0 < d.tiles; b0 += 16) {
-            uint4 x[16];
+    for (int b0 = b_lo; b0 < b_hi; b0 += 16) {
+        uint4 x[16];
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                x[q] = make_uint4(0u, 0u, 0u, 0u);
-                if (b0 + q < d.tiles)
-                    x[q] = *(const uint4 *)(d.counts + (int64_t)(b0 + q) * stride + 4 * t);
-            }
+        for (int q = 0; q < 16; ++q) {
+            x[q] = make_uint4(0u, 0u, 0u, 0u);
+            if (b0 + q < b_hi)
+                x[q] = *(const uint4 *)(d.counts + (int64_t)(b0 + q) * stride + 4 * g);
+        }
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const uint32_t e[4] = {x[q].x, x[q].y, x[q].z, x[q].w};
+        for (int q = 0; q < 16; ++q) {
+            const uint32_t e[4] = {x[q].x, x[q].y, x[q].z, x[q].w};
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    tot[c] += e[c];
-                    pre[c] += b0 + q < tile ? e[c] : 0u;
-                }
+            for (int c = 0; c < 4; ++c) {
+                tot[c] += e[c];
+                pre[c] += b0 + q < tile ? e[c] : 0u;
             }
         }
     }
-    const uint32_t s = tot[0] + tot[1] + tot[2] + tot[3];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        red[0][t][c] = tot[c];
+        red[1][t][c] = pre[c];
+    }
+    __syncthreads();
+    uint32_t s = 0;
+    if (t < groups) {
+        for (int q = 1; q < ranges; ++q)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                tot[c] += red[0][q * groups + t][c];
+                pre[c] += red[1][q * groups + t][c];
+            }
+        s = tot[0] + tot[1] + tot[2] + tot[3];
+    }
     part[t] = s;
     __syncthreads();
     for (int off = 1; off < kSortThreads; off <<= 1) {
@@ -159,108 +163,38 @@ __global__ __launch_bounds__(kSortThreads) void sort_one_pass_kernel(RandomOrder
         part[t] += x;
         __syncthreads();
     }
-    uint32_t run = part[t] - s;
+    if (t < groups) {
+        uint32_t run = part[t] - s;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        base[4 * t + c] = run + pre[c];
-        run += tot[c];
+        for (int c = 0; c < 4; ++c) {
+            base[4 * t + c] = run + pre[c];
+            run += tot[c];
+        }
     }
+    __syncthreads();
+}
+
+// The first pass (see the top of the file): the final order for keys of at most ten bits;
+// else keys and sample indices into the alternate buffers, grouped by their top eight bits,
+// and (workgroup 0) each group's start.
+__global__ __launch_bounds__(kSortThreads) void sort_first_pass_kernel(RandomOrderDesc d)
+{
+    __shared__ uint32_t base[kSortMaxDigits];
+    __shared__ uint32_t wcnt[kSortWaves][kSortMaxDigits];
+    __shared__ uint32_t red[2][kSortThreads][4];
+    __shared__ uint32_t part[kSortThreads];
+    const int t = threadIdx.x;
+    const int ndig = 1 << d.high_bits, low = d.key_bits - d.high_bits;
     for (int v = 0; v < kSortWaves; ++v)
         for (int x = t; x < kSortMaxDigits; x += kSortThreads)
             wcnt[v][x] = 0;
-    __syncthreads();
-    const int64_t first = (int64_t)tile * d.tile, lim = min(first + d.tile, (int64_t)d.n);
-    for (int64_t c0 = first; c0 < lim; c0 += kSortRegs * kSortThreads) {
-        uint32_t key[kSortRegs];
-#pragma unroll
-        for (int k = 0; k < kSortRegs; ++k) {
-            const int64_t j = c0 + k * kSortThreads + t;
-            key[k] = j < lim ? d.keys[j] : 0u;
-        }
-#pragma unroll
-        for (int k = 0; k < kSortRegs; ++k) {
-            if (c0 + k * kSortThreads >= lim)
-                break; // uniform over the workgroup
-            const int64_t j = c0 + k * kSortThreads + t;
-            const bool valid = j < lim;
-            const uint32_t pos = round_place<kSortMaxDigits>(key[k], d.key_bits, valid, base, wcnt);
-            if (valid && pos < (uint32_t)d.n)
-                d.vals[pos] = (uint32_t)j;
-        }
+    tile_bases(d, base, red, part);
+    if (low && blockIdx.x == 0) {
+        for (int x = t; x < ndig; x += kSortThreads)
+            d.seg[x] = base[x];
+        if (t == 0)
+            d.seg[ndig] = (uint32_t)d.n;
     }
-}
-
-// Exclusive scan of the digit-major counts, in place: each of the 1,024 threads loads its
-// contiguous run of at most 64 counts at once (16-byte loads; the count buffer is padded to
-// whole 64-count blocks), the run totals are scanned in LDS, then each run is rewritten.
-__global__ __launch_bounds__(1024) void sort_scan_kernel(RandomOrderDesc d)
-{
-    __shared__ uint32_t part[1024];
-    const int t = threadIdx.x;
-    const int m = (1 << d.high_bits) * d.tiles;
-    const int per = (((m + 1023) / 1024) + 3) & ~3; // <= kScanRegs
-    const int lo = t * per;
-    uint32_t v[kScanRegs];
-    uint32_t s = 0;
-#pragma unroll
-    for (int q = 0; q < kScanRegs / 4; ++q) {
-        const int i = lo + 4 * q;
-        uint4 x = {0u, 0u, 0u, 0u};
-        if (4 * q < per && i < m)
-            x = *(const uint4 *)(d.counts + i);
-        v[4 * q] = i < m ? x.x : 0u;
-        v[4 * q + 1] = i + 1 < m ? x.y : 0u;
-        v[4 * q + 2] = i + 2 < m ? x.z : 0u;
-        v[4 * q + 3] = i + 3 < m ? x.w : 0u;
-    }
-#pragma unroll
-    for (int e = 0; e < kScanRegs; ++e)
-        s += v[e];
-    part[t] = s;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const uint32_t x = t >= off ? part[t - off] : 0u;
-        __syncthreads();
-        part[t] += x;
-        __syncthreads();
-    }
-    uint32_t run = part[t] - s;
-#pragma unroll
-    for (int q = 0; q < kScanRegs / 4; ++q) {
-        const int i = lo + 4 * q;
-        uint4 x;
-        x.x = run;
-        run += v[4 * q];
-        x.y = run;
-        run += v[4 * q + 1];
-        x.z = run;
-        run += v[4 * q + 2];
-        x.w = run;
-        run += v[4 * q + 3];
-        if (4 * q < per && i + 3 < m) {
-            *(uint4 *)(d.counts + i) = x;
-        } else if (4 * q < per && i < m) {
-            d.counts[i] = x.x;
-            if (i + 1 < m)
-                d.counts[i + 1] = x.y;
-            if (i + 2 < m)
-                d.counts[i + 2] = x.z;
-        }
-    }
-}
-
-__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(RandomOrderDesc d)
-{
-    __shared__ uint32_t base[256];
-    __shared__ uint32_t wcnt[kSortWaves][256];
-    const int t = threadIdx.x;
-    const int ndig = 1 << d.high_bits, low = d.key_bits - d.high_bits;
-    base[t] = t < ndig ? d.counts[(int64_t)t * d.tiles + blockIdx.x] : 0u;
-    for (int v = 0; v < kSortWaves; ++v)
-        wcnt[v][t] = 0;
-    __syncthreads();
-    // Keys of more than eight bits go on to the segment pass: this one writes its keys and
-    // sample indices to the alternate buffers; shorter keys are sorted after this pass.
     uint32_t *out = low ? d.vals_alt : d.vals;
     const int64_t first = (int64_t)blockIdx.x * d.tile, lim = min(first + d.tile, (int64_t)d.n);
     for (int64_t c0 = first; c0 < lim; c0 += kSortRegs * kSortThreads) {
@@ -276,7 +210,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(RandomOrderD
                 break; // uniform over the workgroup
             const int64_t j = c0 + k * kSortThreads + t;
             const bool valid = j < lim;
-            const uint32_t pos = round_place<256>(key[k] >> low, d.high_bits, valid, base, wcnt);
+            const uint32_t pos = round_place<kSortMaxDigits>(key[k] >> low, d.high_bits, valid, base, wcnt);
             if (valid && pos < (uint32_t)d.n) {
                 out[pos] = (uint32_t)j;
                 if (low)
@@ -293,8 +227,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_segment_kernel(RandomOrderD
     const int t = threadIdx.x, h = blockIdx.x;
     const int ndig = 1 << d.high_bits, low = d.key_bits - d.high_bits, nlow = 1 << low;
     const uint32_t lmask = (uint32_t)nlow - 1u;
-    const uint32_t start = d.counts[(int64_t)h * d.tiles];
-    const uint32_t end = h + 1 < ndig ? d.counts[(int64_t)(h + 1) * d.tiles] : (uint32_t)d.n;
+    const uint32_t start = d.seg[h], end = d.seg[h + 1];
     base[t] = 0;
     for (int v = 0; v < kSortWaves; ++v)
         wcnt[v][t] = 0;
@@ -366,15 +299,20 @@ int random_order_high_bits(int key_bits, int tiles)
     return key_bits < 8 ? key_bits : 8;
 }
 
+static size_t random_order_seg_offset(int tiles, int high_bits)
+{
+    const size_t ndig = (size_t)1 << high_bits;
+    return ((ndig < 4 ? 4 : ndig) * (size_t)tiles + 63) / 64 * 64;
+}
+
 size_t random_order_count_bytes(int n, int key_bits)
 {
     int tile, tiles;
     random_order_tiles(n, &tile, &tiles);
     const int high = random_order_high_bits(key_bits, tiles);
     const size_t ndig = (size_t)1 << high;
-    // Whole blocks of the scan's 1,024 x 64 counts are read: padded to a multiple of 64.
-    const size_t m = (ndig < 4 ? 4 : ndig) * (size_t)tiles;
-    return (m + 63) / 64 * 64 * sizeof(uint32_t);
+    // The counts, then the first digits' segment starts (two-pass keys).
+    return random_order_seg_offset(tiles, high) * sizeof(uint32_t) + (ndig + 1) * sizeof(uint32_t);
 }
 
 hipError_t launch_random_order(const RandomOrderDesc &d, hipStream_t s, const uint32_t **order)
@@ -384,17 +322,13 @@ hipError_t launch_random_order(const RandomOrderDesc &d, hipStream_t s, const ui
     if (d.n <= 0 || d.key_bits < 1 || d.key_bits > 16 || d.tile != tile || d.tiles != tiles ||
         d.high_bits != random_order_high_bits(d.key_bits, d.tiles))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(sort_count_kernel, dim3((unsigned)d.tiles), dim3(kSortThreads), 0, s, d);
-    if (d.high_bits == d.key_bits) {
-        hipLaunchKernelGGL(sort_one_pass_kernel, dim3((unsigned)d.tiles), dim3(kSortThreads), 0, s, d);
-        *order = d.vals;
-        return hipGetLastError();
-    }
-    hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), 0, s, d);
-    hipLaunchKernelGGL(sort_scatter_kernel, dim3((unsigned)d.tiles), dim3(kSortThreads), 0, s, d);
-    if (d.key_bits > d.high_bits)
-        hipLaunchKernelGGL(sort_segment_kernel, dim3(1u << d.high_bits), dim3(kSortThreads), 0, s, d);
-    *order = d.vals;
+    RandomOrderDesc e = d;
+    e.seg = d.counts + random_order_seg_offset(d.tiles, d.high_bits);
+    hipLaunchKernelGGL(sort_count_kernel, dim3((unsigned)e.tiles), dim3(kSortThreads), 0, s, e);
+    hipLaunchKernelGGL(sort_first_pass_kernel, dim3((unsigned)e.tiles), dim3(kSortThreads), 0, s, e);
+    if (e.key_bits > e.high_bits)
+        hipLaunchKernelGGL(sort_segment_kernel, dim3(1u << e.high_bits), dim3(kSortThreads), 0, s, e);
+    *order = e.vals;
     return hipGetLastError();
 }
 
