@@ -52,8 +52,8 @@ TRAIN_HBM_BYTES_PER_LAUNCH = {0: (7102.0 * 2.0 + 4181.4) * 1024,
 # gradient read-modify-write (2 x that) + the targets' channels at 16 taps x 4 B.
 RANDOM_BYTES_PER_SAMPLE = {2: 2 * 4 * 64 * 3 + 16 * 9 * 4,    # 2,112
                            4: 4 * 4 * 64 * 3 + 16 * 12 * 4}   # 3,840
-TRAIN_HBM_BYTES_RANDOM = {2: (348243.4 * 2.0 + 138384.0) * 1024,    # same counters, config 2 random texels
-                          4: (886018.2 * 2.0 + 1183507.0) * 1024}   # and config 4 random texels (bin-sorted)
+TRAIN_HBM_BYTES_RANDOM = {2: (201679.5 * 2.0 + 138384.0) * 1024,    # same counters, config 2 random texels
+                          4: (885876.8 * 2.0 + 1183510.6) * 1024}   # and config 4 random texels (both bin-sorted)
 # The BC6 block phase's train kernel (the reference network on texels expanded from its
 # BCf-2k block records), same counters.
 TRAIN_HBM_BYTES_BC6 = (9164.0 * 2.0 + 8478.2) * 1024
@@ -232,7 +232,7 @@ def train_entry(lib, nt, ev, cfg, steps, warmup, sample_mode=0, blocks=False):
         # The block phase: records expanded to texels, this kernel, gradients folded back.
         kernel = "train16_kernel<Shape<16,32,2>,3,2,false,false> (BC6 block phase on expanded texels)"
     if sample_mode:
-        kernel = ("train16_kernel<Shape<32,64,2>,16,2,true,false>" if cfg == 2
+        kernel = ("train16_kernel<Shape<32,64,2>,16,2,true,true>" if cfg == 2
                   else "train16_kernel<Shape<64,64,3>,16,2,true,true>")
     if sample_mode:
         # Random texels: bound by scattered memory traffic, priced at the algorithmic bytes

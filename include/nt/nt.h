@@ -247,9 +247,8 @@ int64_t nt_mip_chain_layout(int width, int height, int num_mips, int64_t *mip_of
 /* The same for 4x4 block storage (blocks per dimension = max(size>>2, 1), train.cu:220). */
 int64_t nt_block_chain_layout(int width, int height, int num_mips, int64_t *block_offset);
 /* Bytes of scratch nt_train_step needs for these parameters (0 on error); also enough for
- * nt_inference's fixed-order SSE. A NT_SAMPLES_RANDOM step of a million samples or more also
- * holds its sample sort, sized for the current device (without one, a bound that the step
- * checks against the device's own size). */
+ * nt_inference's fixed-order SSE. A NT_SAMPLES_RANDOM step of 262,144 samples or more also
+ * holds its sample sort (keys, sample indices and per-tile counts, ~12 bytes a sample). */
 size_t nt_train_workspace_bytes(const nt_params *params, nt_kernel_type type);
 
 /* Profiling hook (no reference counterpart): the next nt_train_step, nt_optimize_latents,
@@ -265,7 +264,7 @@ int nt_profile_next_launch(void *start_event, void *stop_event);
  *   flags bit 0 (NT_HOOK_DROP_MARGINS) removes the margin of that kernel's chunk cell box,
  *   which drives its latent scatter's out-of-box path (per-sample global atomics);
  *   flags bit 1 (NT_HOOK_SORT_RANDOM) makes NT_SAMPLES_RANDOM steps sort their samples by
- *   bin at any sample count (they do from a million samples), so that small tests reach
+ *   bin at any sample count (they do from 262,144 samples), so that small tests reach
  *   the sorted order.
  * nt_set_test_hooks(0, 0) restores the defaults. */
 #define NT_HOOK_DROP_MARGINS 1

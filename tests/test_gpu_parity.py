@@ -256,7 +256,7 @@ def test_train_step_scatter_out_of_box_paths(lib, O, shape):
     ("ref", (64, 32), 0, 0, 128), ("c1", (64, 32), 0, 0, 128), ("c2", (64, 32), 0, 0, 128),
     ("c4", (64, 32), 0, 0, 128), ("c2", (50, 13), 2, 0, 128), ("c4", (100, 7), 1, 0, 128),
     ("c2", (100, 30), 2, 0, 128),
-    # the 16-channel kernel's slots in bin order (a step sorts from a million samples)
+    # the 16-channel kernel's slots in bin order (a step sorts from 262,144 samples)
     ("c2", (64, 32), 0, abi.NT_HOOK_SORT_RANDOM, 128), ("c4", (100, 7), 1, abi.NT_HOOK_SORT_RANDOM, 128),
     ("c2", (100, 30), 2, abi.NT_HOOK_SORT_RANDOM, 128),
     # images that are no multiple of the 64-texel bins: partial bins on the right and bottom
@@ -813,7 +813,7 @@ def _run_iterations(lib, a, b, ktype, offs):
     # one per CU for c4), so a different split of the rows would change the sums' bits
     ("c2", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 512, (512, 256), 0),
     ("c4", abi.NT_SAMPLES_REGION, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 512, (512, 256), 0),
-    # random texels in bin order (a step sorts from a million samples): the same sort on both
+    # random texels in bin order (a step sorts from 262,144 samples): the same sort on both
     # paths, so the same slots
     ("c2", abi.NT_SAMPLES_RANDOM, abi.NT_LATENT_TOUCHED, abi.NT_UNCONSTRAINED, False, 128, (64, 32),
      abi.NT_HOOK_SORT_RANDOM),
