@@ -270,6 +270,13 @@ int nt_profile_next_launch(void *start_event, void *stop_event);
 #define NT_HOOK_DROP_MARGINS 1
 #define NT_HOOK_SORT_RANDOM 2
 int nt_set_test_hooks(int max_train_workgroups, int flags);
+/* Test hook (no reference counterpart): the order in which nt_train_step with these
+ * parameters (NT_UNCONSTRAINED) would read its NT_SAMPLES_RANDOM samples, written to
+ * order[0 .. num_samples) on the device: the sample indices sorted stably by the
+ * 64 x 64-texel bin (row-major over the image) of their texels. Uses params->workspace
+ * (nt_train_workspace_bytes). NT_ERR_UNSUPPORTED when the step trains in slot order
+ * (fewer than 262,144 samples without NT_HOOK_SORT_RANDOM, or another kernel). */
+int nt_random_sample_order(const nt_params *params, uint32_t *order, void *stream);
 
 /* ---- the hot path ----------------------------------------------------------------- */
 

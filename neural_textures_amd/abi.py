@@ -170,6 +170,7 @@ SIGNATURES = {
     "nt_block_chain_layout": (C.c_int64, [C.c_int, C.c_int, C.c_int, P(C.c_int64)]),
     "nt_profile_next_launch": (C.c_int, [C.c_void_p, C.c_void_p]),
     "nt_set_test_hooks": (C.c_int, [C.c_int, C.c_int]),
+    "nt_random_sample_order": (C.c_int, [P(nt_params), C.c_void_p, C.c_void_p]),
     "nt_train_workspace_bytes": (C.c_size_t, [P(nt_params), C.c_int]),
     "nt_train_step": (C.c_int, [P(nt_params), C.c_int, C.c_void_p]),
     "nt_train_step_static": (C.c_int, [P(nt_params), C.c_int, C.c_void_p]),

@@ -1045,6 +1045,30 @@ int static_scratch(void **ptr)
 
 // With `deferred` the MLP-gradient reduction is not launched: its descriptor is returned
 // for the caller's combined optimizer launch.
+// The random-texel sort's buffers in the workspace (plan.sort_off != 0).
+static RandomOrderDesc random_order_desc(const nt_params *p, const TrainPlan &plan, uint8_t *ws)
+{
+    const size_t n = (size_t)p->num_samples;
+    const size_t keys = (n * 2 + 255) & ~(size_t)255, vals = (n * 4 + 255) & ~(size_t)255;
+    uint8_t *b = ws + plan.sort_off;
+    RandomOrderDesc r{};
+    r.n = p->num_samples;
+    r.step = (uint32_t)p->step;
+    r.image_w = p->image_width;
+    r.image_h = p->image_height;
+    r.bins_x = plan.sort_bins_x;
+    r.key_bits = plan.sort_key_bits;
+    r.bin_shift = plan.sort_shift;
+    random_order_tiles(r.n, &r.tile, &r.tiles);
+    r.high_bits = random_order_high_bits(r.key_bits, r.tiles);
+    r.keys = (uint16_t *)b;
+    r.keys_alt = (uint16_t *)(b + keys);
+    r.vals = (uint32_t *)(b + 2 * keys);
+    r.vals_alt = (uint32_t *)(b + 2 * keys + vals);
+    r.counts = (uint32_t *)(b + 2 * keys + 2 * vals);
+    return r;
+}
+
 int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const TrainPlan &plan, uint8_t *ws,
                     UpdateLog *log, ReduceDesc *deferred = nullptr)
 {
@@ -1128,25 +1152,7 @@ int train_step_with(const nt_params *p, nt_kernel_type type, void *stream, const
         }
         if (plan.sort_off) {
             // NT_SAMPLES_RANDOM: the slots' samples sorted by bin.
-            const size_t n = (size_t)p->num_samples;
-            const size_t keys = (n * 2 + 255) & ~(size_t)255, vals = (n * 4 + 255) & ~(size_t)255;
-            uint8_t *b = ws + plan.sort_off;
-            RandomOrderDesc r{};
-            r.n = p->num_samples;
-            r.step = (uint32_t)p->step;
-            r.image_w = p->image_width;
-            r.image_h = p->image_height;
-            r.bins_x = plan.sort_bins_x;
-            r.key_bits = plan.sort_key_bits;
-            r.bin_shift = plan.sort_shift;
-            random_order_tiles(r.n, &r.tile, &r.tiles);
-            r.high_bits = random_order_high_bits(r.key_bits, r.tiles);
-            r.keys = (uint16_t *)b;
-            r.keys_alt = (uint16_t *)(b + keys);
-            r.vals = (uint32_t *)(b + 2 * keys);
-            r.vals_alt = (uint32_t *)(b + 2 * keys + vals);
-            r.counts = (uint32_t *)(b + 2 * keys + 2 * vals);
-            e = launch_random_order(r, s, &d.order);
+            e = launch_random_order(random_order_desc(p, plan, ws), s, &d.order);
             if (e != hipSuccess)
                 return hip_status(e, "random-texel sample order");
         }
@@ -1300,6 +1306,33 @@ int nt_train_step(const nt_params *p, nt_kernel_type type, void *stream)
     if (!aligned16(p->workspace))
         return fail(NT_ERR_MISALIGNED, "workspace must be 16-byte aligned");
     return train_step_with(p, type, stream, plan, (uint8_t *)p->workspace, update_log(p));
+}
+
+int nt_random_sample_order(const nt_params *p, uint32_t *order, void *stream)
+{
+    TrainPlan plan;
+    int st = plan_train(p, NT_UNCONSTRAINED, &plan);
+    if (st)
+        return st;
+    if (!order)
+        return fail(NT_ERR_NULL_POINTER, "order");
+    if (!plan.use16 || !plan.sort_off)
+        return fail(NT_ERR_UNSUPPORTED, "these parameters train in slot order (the sort: NT_SAMPLES_RANDOM on the "
+                                        "16-channel kernel, from %d samples or with NT_HOOK_SORT_RANDOM)",
+                    kRandomSortMinSamples);
+    if (!p->workspace || p->workspace_bytes < plan.workspace)
+        return fail(NT_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", plan.workspace,
+                    p->workspace ? p->workspace_bytes : (size_t)0);
+    if (!aligned16(p->workspace))
+        return fail(NT_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t *sorted = nullptr;
+    hipError_t e = launch_random_order(random_order_desc(p, plan, (uint8_t *)p->workspace), s, &sorted);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(order, sorted, (size_t)p->num_samples * sizeof(uint32_t), hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess)
+        return hip_status(e, "random-texel sample order");
+    return NT_OK;
 }
 
 size_t nt_train_static_scratch_bytes(void) { return kStaticScratchBytes; }

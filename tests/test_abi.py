@@ -156,3 +156,24 @@ def test_config_shapes_plan_the_16_channel_kernel(lib, shape, ng, margins):
         assert lib.nt_train_workspace_bytes(C.byref(p), 0) == tiles * P_total * 4
     finally:
         assert lib.nt_set_test_hooks(0, 0) == 0
+
+
+def test_random_sample_order_refusals(lib):
+    """nt_random_sample_order refuses, before touching a device, parameters that train in
+    slot order (random texels below the sort's sample count without the hook, region
+    samples) and a null order buffer."""
+    from helpers import make_state
+    st = make_state("c2", image=256, region=(64, 64))
+    st.sample_mode = abi.NT_SAMPLES_RANDOM
+    p = st.params()
+    order = np.zeros(64 * 64, np.uint32)
+    assert lib.nt_random_sample_order(C.byref(p), C.c_void_p(order.ctypes.data), None) == abi.NT_ERR_UNSUPPORTED
+    assert b"slot order" in lib.nt_last_error()
+    region = make_state("c2", image=256, region=(64, 64)).params()
+    assert lib.nt_set_test_hooks(0, abi.NT_HOOK_SORT_RANDOM) == 0
+    try:
+        assert lib.nt_random_sample_order(C.byref(region), C.c_void_p(order.ctypes.data), None) == abi.NT_ERR_UNSUPPORTED
+        assert lib.nt_random_sample_order(C.byref(p), None, None) == abi.NT_ERR_NULL_POINTER
+        assert lib.nt_random_sample_order(C.byref(p), C.c_void_p(order.ctypes.data), None) == abi.NT_ERR_WORKSPACE
+    finally:
+        assert lib.nt_set_test_hooks(0, 0) == 0

@@ -312,6 +312,41 @@ def test_random_texel_sorted_step_is_deterministic(lib):
         assert_close(to_np(gb.grads), to_np(ga.grads), "latent grads of two runs", tol=1e-5, floor=1e-6)
 
 
+@pytest.mark.parametrize("image,region", [(128, (128, 100)), (2112, (100, 100)), (168, (64, 32))],
+                         ids=["one-pass-4tiles", "two-pass", "partial-bins"])
+def test_random_sample_order_is_the_stable_bin_sort(lib, O, image, region):
+    """The order a sorted NT_SAMPLES_RANDOM step reads its samples in, exactly (integer
+    work): the sample indices sorted stably by the 64 x 64-texel bin, row-major, of each
+    sample's texel, the texel from the oracle's seed and hash (the placement the oracle's
+    own position test pins against ntref_sample_uvz)."""
+    import torch
+    say(f"case: random sample order image {image} region {region}")
+    st = make_state("c2", image=image, region=region, seed=29, step=7)
+    st.sample_mode = abi.NT_SAMPLES_RANDOM
+    nt.check(lib.nt_set_test_hooks(0, abi.NT_HOOK_SORT_RANDOM))
+    try:
+        g = gpu_workspace(lib, st.to_torch(), abi.NT_UNCONSTRAINED)
+        n = st.num_samples
+        order = torch.full((n,), -1, dtype=torch.int32, device="cuda")
+        nt.check(lib.nt_random_sample_order(C.byref(g.params()), C.c_void_p(order.data_ptr()), None))
+        sync()
+    finally:
+        nt.check(lib.nt_set_test_hooks(0, 0))
+    W = H = image
+    key = np.empty(n, np.int64)
+    for i in range(n):
+        h1 = O.ntref_fmix32(O.ntref_sample_seed(i, 7))
+        h2 = O.ntref_fmix32(h1)
+        u0 = np.float32(h1 & 0xFFFFFF) * np.float32(2.0 ** -24)
+        u1 = np.float32(h2 & 0xFFFFFF) * np.float32(2.0 ** -24)
+        x, y = min(int(np.float32(u0) * np.float32(W)), W - 1), min(int(np.float32(u1) * np.float32(H)), H - 1)
+        key[i] = (y >> 6) * ((W + 63) // 64) + (x >> 6)
+    expected = np.argsort(key, kind="stable")
+    got = order.cpu().numpy().astype(np.int64)
+    assert np.array_equal(got, expected)
+    assert len(np.unique(key)) > 1
+
+
 def test_train_step_accumulates(lib, O):
     """Two passes without an optimizer step add up (the zero-gradient contract)."""
     say("case: train accumulate")
