@@ -38,11 +38,25 @@ def _zero(s):
         a.zero_()
 
 
-@pytest.mark.parametrize("shape", ["c4", "c2", "ref", "ref16f"])
+@pytest.mark.parametrize("shape", ["c4", "c2", "ref", "ref16f", "c2-random-sorted"])
 def test_static_scratch_matches_workspace_step(lib, shape):
+    """c2-random-sorted: random texels in bin order (the sort's buffers in the static array
+    too): both entry points read the samples in the same order."""
     import torch
     assert lib.nt_train_static_scratch_bytes() == 32 << 20
-    st = make_state(shape, image=256, region=(128, 64), seed=3, offset=(40, 17), step=5)
+    sorted_random = shape.endswith("-random-sorted")
+    st = make_state(shape.split("-")[0], image=256, region=(128, 64), seed=3, offset=(40, 17), step=5)
+    if sorted_random:
+        st.sample_mode = abi.NT_SAMPLES_RANDOM
+    nt.check(lib.nt_set_test_hooks(0, abi.NT_HOOK_SORT_RANDOM if sorted_random else 0))
+    try:
+        _static_matches_workspace(lib, shape, st)
+    finally:
+        nt.check(lib.nt_set_test_hooks(0, 0))
+
+
+def _static_matches_workspace(lib, shape, st):
+    import torch
     with_ws = gpu_workspace(lib, st.to_torch(), abi.NT_UNCONSTRAINED)
     static = st.to_torch()  # no workspace
     for region, offset in (((128, 64), (40, 17)), ((64, 16), (9, 201))):  # the second is smaller
