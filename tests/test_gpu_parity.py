@@ -312,8 +312,10 @@ def test_random_texel_sorted_step_is_deterministic(lib):
         assert_close(to_np(gb.grads), to_np(ga.grads), "latent grads of two runs", tol=1e-5, floor=1e-6)
 
 
-@pytest.mark.parametrize("image,region", [(128, (128, 100)), (2112, (100, 100)), (168, (64, 32))],
-                         ids=["one-pass-4tiles", "two-pass", "partial-bins"])
+@pytest.mark.parametrize("image,region", [(128, (128, 100)), (2112, (100, 100)), (168, (64, 32)),
+                                          (2048, (512, 512)), (4096, (1024, 1024))],
+                         ids=["one-pass-4tiles", "two-pass", "partial-bins", "config2-full-size",
+                              "config4-size-two-pass"])
 def test_random_sample_order_is_the_stable_bin_sort(lib, O, image, region):
     """The order a sorted NT_SAMPLES_RANDOM step reads its samples in, exactly (integer
     work): the sample indices sorted stably by the 64 x 64-texel bin, row-major, of each
@@ -333,6 +335,8 @@ def test_random_sample_order_is_the_stable_bin_sort(lib, O, image, region):
     finally:
         nt.check(lib.nt_set_test_hooks(0, 0))
     W = H = image
+    # config 2's full size: 262,144 samples, 1,024 bins, 64 tiles, one pass; config 4's
+    # sample count and image: 1,048,576 samples, 4,096 bins, 256 tiles, two passes
     key = np.empty(n, np.int64)
     for i in range(n):
         h1 = O.ntref_fmix32(O.ntref_sample_seed(i, 7))
